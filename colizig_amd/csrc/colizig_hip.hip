@@ -1,0 +1,1048 @@
+// colizig_hip.hip - libcolizig_hip.so: colizig's block-FP8 MoE expert path on
+// MI355X (gfx950), behind colizig's src/backend C-ABI (include/colizig_hip.h).
+//
+// One global context (as the CUDA DLL, colizig_cuda.cu:80-106), one HIP
+// stream at default priority.  Every entry point saves/restores the host
+// MXCSR (colizig_cuda.cu:22-29): the GPU runtime must not leak FTZ/DAZ into
+// the engine's CPU float math.
+#include "cz_kernels.h"
+#include "colizig_hip.h"
+
+#include <xmmintrin.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+struct CsrGuard {
+    unsigned saved;
+    CsrGuard() : saved(_mm_getcsr()) {}
+    ~CsrGuard() { _mm_setcsr(saved); }
+};
+
+inline uint32_t nblk(uint32_t x) { return (x + CZ_BLOCK - 1) / CZ_BLOCK; }
+
+// ---- keyed HBM weight cache for the per-matmul ABI (colizig_cuda.cu:80-169)
+struct Slot {
+    uint64_t key = 0;  // 0 = free
+    void *w = nullptr;
+    size_t wcap = 0;
+    void *s = nullptr;
+    size_t scap = 0;
+    uint64_t clock = 0;
+};
+constexpr size_t kMaxSlots = 4096;
+
+// ---- one registered MoE layer
+struct LayerHost {
+    colizig_dims d{};
+    float *router = nullptr;
+    uint8_t *ew = nullptr;
+    float *es = nullptr;
+    uint8_t *sw = nullptr;
+    float *ss = nullptr;
+    float *shg = nullptr;
+    std::vector<uint8_t> loaded;
+    uint32_t nloaded = 0;
+    bool shared_set = false;
+
+    uint64_t ew_stride() const { return 3ull * d.inter * d.hidden; }
+    uint64_t es_stride() const { return 3ull * nblk(d.inter) * nblk(d.hidden); }
+    uint64_t sw_bytes() const { return 3ull * d.shared_inter * d.hidden; }
+    uint64_t ss_floats() const { return 3ull * nblk(d.shared_inter) * nblk(d.hidden); }
+    bool ready() const { return nloaded == d.experts && (d.shared_inter == 0 || shared_set); }
+    LayerDev dev() const {
+        LayerDev L{};
+        L.H = d.hidden;
+        L.E = d.experts;
+        L.K = d.topk;
+        L.I = d.inter;
+        L.SI = d.shared_inter;
+        L.norm_topk = d.norm_topk;
+        L.nbH = nblk(d.hidden);
+        L.nbI = nblk(d.inter);
+        L.nbSI = nblk(d.shared_inter);
+        L.router = router;
+        L.ew = ew;
+        L.es = es;
+        L.ew_stride = ew_stride();
+        L.es_stride = es_stride();
+        L.sw = sw;
+        L.ss = ss;
+        L.sh_gate = shg;
+        return L;
+    }
+};
+
+// ---- device scratch of a forward (grow-only; retired buffers live until
+// shutdown so a captured graph never points at freed memory)
+struct Work {
+    float *xin = nullptr, *out = nullptr, *xn = nullptr, *logits = nullptr, *gates = nullptr, *sgate = nullptr;
+    float *h = nullptr, *hs = nullptr;
+    uint32_t *idx = nullptr, *counters = nullptr;
+    size_t cap_xin = 0, cap_out = 0, cap_xn = 0, cap_logits = 0, cap_idx = 0, cap_gates = 0, cap_sgate = 0,
+           cap_cnt = 0, cap_h = 0, cap_hs = 0;
+};
+
+struct Ctx {
+    int inited = 0;
+    char name[192] = {0};
+    hipStream_t stream = nullptr;
+    // per-matmul ABI buffers
+    void *d_x = nullptr, *d_y = nullptr, *d_w = nullptr, *d_s = nullptr;
+    size_t d_x_cap = 0, d_y_cap = 0, d_w_cap = 0, d_s_cap = 0;
+    void *h_stage = nullptr;  // pinned staging for x / y
+    size_t h_stage_cap = 0;
+    // keyed cache
+    uint64_t budget = 0, used = 0, lru = 0;
+    std::vector<Slot> slots;
+    std::unordered_map<uint64_t, int> by_key;
+    uint64_t hits = 0, misses = 0, uploaded = 0;
+    // MoE layers
+    std::unordered_map<uint32_t, LayerHost> layers;
+    Work work;
+    std::vector<void *> retired;
+    std::unordered_map<int64_t, hipGraphExec_t> graphs;
+    std::unordered_map<int64_t, hipGraph_t> graph_defs;
+    std::unordered_map<int64_t, hipEvent_t> events;
+    int64_t next_handle = 1;
+};
+
+Ctx g;
+std::recursive_mutex g_mu;
+char g_err[512] = {0};
+
+#define CZ_CHECK(call, rc)                                                   \
+    do {                                                                     \
+        hipError_t e_ = (call);                                              \
+        if (e_ != hipSuccess) {                                              \
+            snprintf(g_err, sizeof g_err, "%s: %s", #call, hipGetErrorString(e_)); \
+            return (rc);                                                     \
+        }                                                                    \
+    } while (0)
+
+int ensure_dev(void **p, size_t *cap, size_t need) {
+    if (*cap >= need) return 0;
+    if (*p) {
+        if (hipFree(*p) != hipSuccess) {}
+    }
+    *p = nullptr;
+    *cap = 0;
+    if (hipMalloc(p, need) != hipSuccess) {
+        *p = nullptr;
+        return -1;
+    }
+    *cap = need;
+    return 0;
+}
+
+int ensure_host(size_t need) {
+    if (g.h_stage_cap >= need) return 0;
+    if (g.h_stage) (void)hipHostFree(g.h_stage);
+    g.h_stage = nullptr;
+    g.h_stage_cap = 0;
+    if (hipHostMalloc(&g.h_stage, need, hipHostMallocDefault) != hipSuccess) {
+        g.h_stage = nullptr;
+        return -1;
+    }
+    g.h_stage_cap = need;
+    return 0;
+}
+
+template <typename T>
+int grow(T **p, size_t *cap, size_t need, bool zero) {
+    if (*cap >= need) return 0;
+    if (*p) g.retired.push_back((void *)*p);
+    *p = nullptr;
+    *cap = 0;
+    void *q = nullptr;
+    if (hipMalloc(&q, need * sizeof(T)) != hipSuccess) return -1;
+    if (zero && hipMemset(q, 0, need * sizeof(T)) != hipSuccess) return -1;
+    *p = (T *)q;
+    *cap = need;
+    return 0;
+}
+
+// Scratch for S tokens of a layer with dims d (max over callers).
+int ensure_work(const colizig_dims &d, int S) {
+    Work &w = g.work;
+    const size_t s = (size_t)S;
+    const size_t tiles = s;  // router token tiles are at least one token wide
+    if (grow(&w.xin, &w.cap_xin, s * d.hidden, false) || grow(&w.out, &w.cap_out, s * d.hidden, false) ||
+        grow(&w.xn, &w.cap_xn, s * d.hidden, false) || grow(&w.logits, &w.cap_logits, s * d.experts, false) ||
+        grow(&w.idx, &w.cap_idx, s * d.topk, false) || grow(&w.gates, &w.cap_gates, s * d.topk, false) ||
+        grow(&w.sgate, &w.cap_sgate, s, false) || grow(&w.counters, &w.cap_cnt, tiles, true) ||
+        grow(&w.h, &w.cap_h, s * d.topk * (size_t)d.inter, false) ||
+        grow(&w.hs, &w.cap_hs, std::max<size_t>(1, s * d.shared_inter), false)) {
+        snprintf(g_err, sizeof g_err, "scratch allocation failed (S=%d)", S);
+        return -2;
+    }
+    return 0;
+}
+
+void free_layer(LayerHost &L) {
+    for (void *p : {(void *)L.router, (void *)L.ew, (void *)L.es, (void *)L.sw, (void *)L.ss, (void *)L.shg})
+        if (p) (void)hipFree(p);
+    L = LayerHost{};
+}
+
+hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g.stream; }
+
+// ---- launches of one layer ------------------------------------------------
+// Router token tile: tt tokens of H floats staged in LDS, kept <= 32 KiB.
+int router_tokens_per_tile(uint32_t H) {
+    return (int)std::min<uint32_t>(CZ_ROUTER_TT, std::max<uint32_t>(1u, 8192u / std::max<uint32_t>(H, 1u)));
+}
+
+template <int NB>
+void launch_up(const LayerDev &L, const float *xn, const uint32_t *idx, float *h, float *hs, int S, hipStream_t st) {
+    constexpr int RW = 2;
+    const uint32_t rows_wg = 4 * RW;
+    const uint32_t blocks = (uint32_t)S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
+                            (L.SI ? (uint32_t)S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
+    k_up_fast<NB, RW><<<blocks, 256, 0, st>>>(L, xn, idx, h, hs, S);
+}
+
+template <int NBI, int NBS>
+void launch_down(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
+                 const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
+    constexpr int RD = 2;
+    const uint32_t rows_wg = 4 * RD;
+    const uint32_t blocks = (uint32_t)S * ((L.H + rows_wg - 1) / rows_wg);
+    k_down_fast<NBI, NBS, RD><<<blocks, 256, 0, st>>>(L, h, hs, idx, gates, sgate, xres, out, S);
+}
+
+bool up_fast(const LayerDev &L, const float *xn, const uint32_t *idx, float *h, float *hs, int S, hipStream_t st) {
+    if (L.H % 64) return false;
+    switch (L.H / 64) {
+        case 4: launch_up<4>(L, xn, idx, h, hs, S, st); return true;
+        case 8: launch_up<8>(L, xn, idx, h, hs, S, st); return true;
+        case 16: launch_up<16>(L, xn, idx, h, hs, S, st); return true;
+        case 32: launch_up<32>(L, xn, idx, h, hs, S, st); return true;
+        case 48: launch_up<48>(L, xn, idx, h, hs, S, st); return true;
+        case 64: launch_up<64>(L, xn, idx, h, hs, S, st); return true;
+        default: return false;
+    }
+}
+
+template <int NBI>
+bool down_fast_s(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
+                 const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
+    if (L.SI == 0) { launch_down<NBI, 0>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true; }
+    if (L.SI % 64) return false;
+    switch (L.SI / 64) {
+        case 8: launch_down<NBI, 8>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
+        case 16: launch_down<NBI, 16>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
+        case 32: launch_down<NBI, 32>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
+        case 64: launch_down<NBI, 64>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
+        default: return false;
+    }
+}
+
+bool down_fast(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
+               const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
+    if (L.I % 64) return false;
+    switch (L.I / 64) {
+        case 4: return down_fast_s<4>(L, h, hs, idx, gates, sgate, xres, out, S, st);
+        case 8: return down_fast_s<8>(L, h, hs, idx, gates, sgate, xres, out, S, st);
+        case 12: return down_fast_s<12>(L, h, hs, idx, gates, sgate, xres, out, S, st);
+        case 16: return down_fast_s<16>(L, h, hs, idx, gates, sgate, xres, out, S, st);
+        default: return false;
+    }
+}
+
+// x: router input (rms=0) or residual (rms=1); out may alias xres.
+// ev (nullable): six events recorded before/after the router, up and down
+// kernels, for the per-kernel timing pass.
+int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                 float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st,
+                 hipEvent_t *ev = nullptr) {
+    const LayerDev L = Lh.dev();
+    Work &w = g.work;
+    RouterArgs A{};
+    A.L = L;
+    A.x = x;
+    A.xn = w.xn;
+    A.logits = w.logits;
+    A.idx = w.idx;
+    A.gates = w.gates;
+    A.sgate = w.sgate;
+    A.counters = w.counters;
+    A.idx_trace = idx_trace;
+    A.gates_trace = gates_trace;
+    A.xn_trace = xn_trace;
+    A.S = S;
+    A.rms = rms;
+    A.eps = eps;
+    const int tt = router_tokens_per_tile(L.H);
+    A.tt = tt;
+    const dim3 rgrid((L.E + 7) / 8, (S + tt - 1) / tt);
+    const size_t lds = std::max<size_t>((size_t)tt * L.H, 4 * CZ_MAX_E) * sizeof(float);
+    if (ev) (void)hipEventRecord(ev[0], st);
+    k_router<<<rgrid, 256, lds, st>>>(A);
+    if (ev) (void)hipEventRecord(ev[1], st);
+    const float *xn = rms ? w.xn : x;
+    if (ev) (void)hipEventRecord(ev[2], st);
+    if (!up_fast(L, xn, w.idx, w.h, w.hs, S, st)) {
+        const uint32_t blocks = (uint32_t)S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)S * ((L.SI + 3) / 4) : 0u);
+        k_up_generic<<<blocks, 256, 0, st>>>(L, xn, w.idx, w.h, w.hs, S);
+    }
+    if (ev) (void)hipEventRecord(ev[3], st);
+    if (ev) (void)hipEventRecord(ev[4], st);
+    if (!down_fast(L, w.h, w.hs, w.idx, w.gates, w.sgate, xres, out, S, st)) {
+        const uint32_t blocks = (uint32_t)S * ((L.H + 3) / 4);
+        k_down_generic<<<blocks, 256, 0, st>>>(L, w.h, w.hs, w.idx, w.gates, w.sgate, xres, out, S);
+    }
+    if (ev) (void)hipEventRecord(ev[5], st);
+    if (hipGetLastError() != hipSuccess) return -4;
+    return 0;
+}
+
+LayerHost *find_layer(uint32_t layer) {
+    auto it = g.layers.find(layer);
+    return it == g.layers.end() ? nullptr : &it->second;
+}
+
+int check_layer_ready(LayerHost *L, uint32_t layer) {
+    if (!L) {
+        snprintf(g_err, sizeof g_err, "layer %u not registered", layer);
+        return -6;
+    }
+    if (!L->ready()) {
+        snprintf(g_err, sizeof g_err, "layer %u: %u of %u experts loaded%s", layer, L->nloaded, L->d.experts,
+                 (L->d.shared_inter && !L->shared_set) ? ", shared expert missing" : "");
+        return -6;
+    }
+    if (L->d.experts > CZ_MAX_E || L->d.topk > CZ_MAX_K || L->d.topk == 0 || L->d.topk > L->d.experts) {
+        snprintf(g_err, sizeof g_err, "layer %u: experts %u / topk %u outside the supported range", layer,
+                 L->d.experts, L->d.topk);
+        return -1;
+    }
+    if (L->d.hidden > 8192) {
+        snprintf(g_err, sizeof g_err, "layer %u: hidden %u > 8192", layer, L->d.hidden);
+        return -1;
+    }
+    return 0;
+}
+
+uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+// synthetic generator over one role of every expert of a layer
+__global__ __launch_bounds__(256) void k_synth_fp8_experts(uint8_t *ew, float *es, uint64_t ew_stride,
+                                                           uint64_t es_stride, uint64_t w_off, uint64_t s_off,
+                                                           uint32_t rows, uint32_t cols, uint64_t seed, float stdv);
+
+// ===========================================================================
+// 1. the existing backend ABI
+// ===========================================================================
+extern "C" int colizig_cuda_init(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (g.inited) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        snprintf(g_err, sizeof g_err, "no HIP device");
+        return -1;
+    }
+    if (hipSetDevice(0) != hipSuccess) return -2;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return -3;
+    snprintf(g.name, sizeof g.name, "%s (%s, %zu MiB)", prop.name, prop.gcnArchName,
+             (size_t)(prop.totalGlobalMem >> 20));
+    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) return -4;
+    g.budget = 0;  // keyed cache off until set (colizig_cuda.cu:185)
+    g.inited = 1;
+    return 0;
+}
+
+extern "C" const char *colizig_cuda_device_name(void) { return g.inited ? g.name : ""; }
+
+extern "C" void colizig_cuda_set_vram_budget(uint64_t bytes) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited) return;
+    size_t freeb = 0, totalb = 0;
+    if (hipMemGetInfo(&freeb, &totalb) == hipSuccess && bytes > freeb - (freeb / 8)) bytes = freeb - (freeb / 8);
+    g.budget = bytes;
+}
+
+extern "C" void colizig_cuda_stats(uint64_t *hits, uint64_t *misses, uint64_t *uploaded_mib, uint64_t *resident) {
+    if (hits) *hits = g.hits;
+    if (misses) *misses = g.misses;
+    if (uploaded_mib) *uploaded_mib = g.uploaded >> 20;
+    if (resident) *resident = (uint64_t)g.slots.size();
+}
+
+extern "C" void colizig_cuda_shutdown(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited) return;
+    (void)hipStreamSynchronize(g.stream);
+    for (auto &kv : g.graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto &kv : g.graph_defs) (void)hipGraphDestroy(kv.second);
+    for (auto &kv : g.events) (void)hipEventDestroy(kv.second);
+    for (auto &kv : g.layers) free_layer(kv.second);
+    for (Slot &s : g.slots) {
+        if (s.w) (void)hipFree(s.w);
+        if (s.s) (void)hipFree(s.s);
+    }
+    for (void *p : {g.d_x, g.d_y, g.d_w, g.d_s}) if (p) (void)hipFree(p);
+    if (g.h_stage) (void)hipHostFree(g.h_stage);
+    Work &w = g.work;
+    for (void *p : {(void *)w.xin, (void *)w.out, (void *)w.xn, (void *)w.logits, (void *)w.gates,
+                    (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx, (void *)w.counters})
+        if (p) (void)hipFree(p);
+    for (void *p : g.retired) (void)hipFree(p);
+    (void)hipStreamDestroy(g.stream);
+    g.~Ctx();
+    new (&g) Ctx();
+}
+
+// Slot for `key` (hit), or a slot to fill (colizig_cuda.cu:132-169 policy:
+// fresh slot within budget, else the LRU slot whose buffers fit, else grow
+// the globally LRU slot).  -1 when nothing can be allocated.
+static int cache_slot_for(uint64_t key, size_t wb, size_t sb) {
+    auto it = g.by_key.find(key);
+    if (it != g.by_key.end()) return it->second;
+    if (g.slots.size() < kMaxSlots && g.used + wb + sb <= g.budget) {
+        Slot s;
+        if (ensure_dev(&s.w, &s.wcap, wb) || ensure_dev(&s.s, &s.scap, sb)) {
+            if (s.w) (void)hipFree(s.w);
+            if (s.s) (void)hipFree(s.s);
+            return -1;
+        }
+        g.used += s.wcap + s.scap;
+        g.slots.push_back(s);
+        return (int)g.slots.size() - 1;
+    }
+    int victim = -1;
+    uint64_t best = ~0ull;
+    for (size_t i = 0; i < g.slots.size(); ++i)
+        if (g.slots[i].wcap >= wb && g.slots[i].scap >= sb && g.slots[i].clock < best) {
+            best = g.slots[i].clock;
+            victim = (int)i;
+        }
+    if (victim < 0) {
+        for (size_t i = 0; i < g.slots.size(); ++i)
+            if (g.slots[i].clock < best) {
+                best = g.slots[i].clock;
+                victim = (int)i;
+            }
+        if (victim < 0) return -1;
+        Slot &s = g.slots[victim];
+        g.used -= s.wcap + s.scap;
+        if (ensure_dev(&s.w, &s.wcap, wb) || ensure_dev(&s.s, &s.scap, sb)) return -1;
+        g.used += s.wcap + s.scap;
+    }
+    if (g.slots[victim].key) g.by_key.erase(g.slots[victim].key);
+    g.slots[victim].key = 0;
+    return victim;
+}
+
+extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, const float *scales, int S,
+                                       int I, int O, uint64_t key) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || I < 1 || O < 1 || !y || !x || !w || !scales) return -1;
+    const size_t nbi = nblk((uint32_t)I), nbo = nblk((uint32_t)O);
+    const size_t xb = (size_t)S * I * sizeof(float), wb = (size_t)O * I, sb = nbo * nbi * sizeof(float),
+                 yb = (size_t)S * O * sizeof(float);
+    if (ensure_dev(&g.d_x, &g.d_x_cap, xb) || ensure_dev(&g.d_y, &g.d_y_cap, yb)) return -2;
+    if (ensure_host(std::max(xb, yb))) return -2;
+    memcpy(g.h_stage, x, xb);
+    if (hipMemcpyAsync(g.d_x, g.h_stage, xb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
+    const void *wdev = nullptr, *sdev = nullptr;
+    if (key != 0 && g.budget != 0) {
+        const int i = cache_slot_for(key, wb, sb);
+        if (i < 0) {
+            key = 0;  // cache full of bigger blocks: uncached path
+        } else if (g.slots[i].key == key) {
+            g.hits++;
+            g.slots[i].clock = ++g.lru;
+            wdev = g.slots[i].w;
+            sdev = g.slots[i].s;
+        } else {
+            g.misses++;
+            if (hipMemcpyAsync(g.slots[i].w, w, wb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
+            if (hipMemcpyAsync(g.slots[i].s, scales, sb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
+            g.uploaded += wb + sb;
+            g.slots[i].key = key;
+            g.by_key[key] = i;
+            g.slots[i].clock = ++g.lru;
+            wdev = g.slots[i].w;
+            sdev = g.slots[i].s;
+        }
+    }
+    if (key == 0 || g.budget == 0) {
+        if (ensure_dev(&g.d_w, &g.d_w_cap, wb) || ensure_dev(&g.d_s, &g.d_s_cap, sb)) return -2;
+        if (hipMemcpyAsync(g.d_w, w, wb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
+        if (hipMemcpyAsync(g.d_s, scales, sb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
+        g.uploaded += wb + sb;
+        wdev = g.d_w;
+        sdev = g.d_s;
+    }
+    k_gemm_fp8_generic<<<(O + 3) / 4, 256, 0, g.stream>>>((float *)g.d_y, (const float *)g.d_x,
+                                                          (const uint8_t *)wdev, (const float *)sdev, S, I, O);
+    if (hipGetLastError() != hipSuccess) return -4;
+    if (hipMemcpyAsync(g.h_stage, g.d_y, yb, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return -5;
+    if (hipStreamSynchronize(g.stream) != hipSuccess) return -5;
+    memcpy(y, g.h_stage, yb);
+    return 0;
+}
+
+// ===========================================================================
+// 2. MoE-level extensions
+// ===========================================================================
+extern "C" int colizig_hip_dequant_fp8(float *out, const unsigned char *w, const float *scales, int rows, int cols) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || rows < 1 || cols < 1 || !out || !w || !scales) return -1;
+    const size_t n = (size_t)rows * cols, sb = (size_t)nblk(rows) * nblk(cols) * sizeof(float);
+    void *dw = nullptr, *ds = nullptr, *dout = nullptr;
+    int rc = 0;
+    if (hipMalloc(&dw, (n + 3) & ~(size_t)3) != hipSuccess || hipMalloc(&ds, sb) != hipSuccess ||
+        hipMalloc(&dout, n * sizeof(float)) != hipSuccess) {
+        rc = -2;
+        goto done;
+    }
+    if (hipMemcpy(dw, w, n, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ds, scales, sb, hipMemcpyHostToDevice) != hipSuccess) {
+        rc = -3;
+        goto done;
+    }
+    {
+        const uint64_t work = (cols % 4 == 0) ? n / 4 : n;
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>((work + 255) / 256, 65536);
+        k_dequant_fp8<<<blocks, 256, 0, g.stream>>>((float *)dout, (const uint8_t *)dw, (const float *)ds,
+                                                    (uint32_t)rows, (uint32_t)cols, nblk(cols));
+        if (hipGetLastError() != hipSuccess) {
+            rc = -4;
+            goto done;
+        }
+        if (hipStreamSynchronize(g.stream) != hipSuccess ||
+            hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+            rc = -5;
+    }
+done:
+    if (dw) (void)hipFree(dw);
+    if (ds) (void)hipFree(ds);
+    if (dout) (void)hipFree(dout);
+    return rc;
+}
+
+extern "C" int colizig_hip_layer_init(uint32_t layer, const colizig_dims *dims, const float *router) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !dims) return -1;
+    const colizig_dims d = *dims;
+    if (d.hidden == 0 || d.experts == 0 || d.topk == 0 || d.inter == 0 || d.topk > d.experts ||
+        d.experts > CZ_MAX_E || d.topk > CZ_MAX_K || d.hidden > 8192) {
+        snprintf(g_err, sizeof g_err, "unsupported dims H=%u E=%u K=%u I=%u", d.hidden, d.experts, d.topk, d.inter);
+        return -1;
+    }
+    (void)hipStreamSynchronize(g.stream);
+    auto it = g.layers.find(layer);
+    if (it != g.layers.end()) free_layer(it->second);
+    LayerHost &L = g.layers[layer];
+    L.d = d;
+    if (hipMalloc(&L.router, (size_t)d.experts * d.hidden * sizeof(float)) != hipSuccess ||
+        hipMalloc(&L.ew, L.ew_stride() * d.experts) != hipSuccess ||
+        hipMalloc(&L.es, L.es_stride() * d.experts * sizeof(float)) != hipSuccess) {
+        free_layer(L);
+        g.layers.erase(layer);
+        snprintf(g_err, sizeof g_err, "layer %u: HBM allocation failed", layer);
+        return -2;
+    }
+    if (d.shared_inter) {
+        if (hipMalloc(&L.sw, L.sw_bytes()) != hipSuccess || hipMalloc(&L.ss, L.ss_floats() * sizeof(float)) != hipSuccess ||
+            hipMalloc(&L.shg, (size_t)d.hidden * sizeof(float)) != hipSuccess) {
+            free_layer(L);
+            g.layers.erase(layer);
+            return -2;
+        }
+    }
+    L.loaded.assign(d.experts, 0);
+    if (router) {
+        if (hipMemcpy(L.router, router, (size_t)d.experts * d.hidden * sizeof(float), hipMemcpyHostToDevice) !=
+            hipSuccess)
+            return -3;
+    }
+    return 0;
+}
+
+extern "C" int colizig_hip_expert_load(uint32_t layer, uint32_t expert, const unsigned char *gate_w,
+                                       const float *gate_s, const unsigned char *up_w, const float *up_s,
+                                       const unsigned char *down_w, const float *down_s) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || expert >= L->d.experts || !gate_w || !gate_s || !up_w || !up_s || !down_w || !down_s)
+        return -1;
+    const uint64_t mb = (uint64_t)L->d.inter * L->d.hidden;
+    const uint64_t nsc = (uint64_t)nblk(L->d.inter) * nblk(L->d.hidden);
+    uint8_t *wb = L->ew + expert * L->ew_stride();
+    float *sb = L->es + expert * L->es_stride();
+    CZ_CHECK(hipMemcpyAsync(wb, gate_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(wb + mb, up_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(wb + 2 * mb, down_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(sb, gate_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(sb + nsc, up_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(sb + 2 * nsc, down_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    if (!L->loaded[expert]) {
+        L->loaded[expert] = 1;
+        L->nloaded++;
+    }
+    return 0;
+}
+
+extern "C" int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char *gate_w, const float *gate_s,
+                                            const unsigned char *up_w, const float *up_s,
+                                            const unsigned char *down_w, const float *down_s,
+                                            const float *sh_gate) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || L->d.shared_inter == 0 || !gate_w || !gate_s || !up_w || !up_s || !down_w || !down_s ||
+        !sh_gate)
+        return -1;
+    const uint64_t mb = (uint64_t)L->d.shared_inter * L->d.hidden;
+    const uint64_t nsc = (uint64_t)nblk(L->d.shared_inter) * nblk(L->d.hidden);
+    CZ_CHECK(hipMemcpyAsync(L->sw, gate_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->sw + mb, up_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->sw + 2 * mb, down_w, mb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->ss, gate_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->ss + nsc, up_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->ss + 2 * nsc, down_s, nsc * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(L->shg, sh_gate, (size_t)L->d.hidden * 4, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    L->shared_set = true;
+    return 0;
+}
+
+extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, int S, float *out_dev,
+                                           uint32_t *idx_dev, float *gates_dev, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x_dev || !out_dev) return -1;
+    LayerHost *L = find_layer(layer);
+    int rc = check_layer_ready(L, layer);
+    if (rc) return rc;
+    if ((rc = ensure_work(L->d, S))) return rc;
+    return launch_layer(*L, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, idx_dev, gates_dev, pick_stream(stream));
+}
+
+extern "C" int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, uint32_t *routed_idx,
+                                       float *routed_gates) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x || !out) return -1;
+    LayerHost *L = find_layer(layer);
+    int rc = check_layer_ready(L, layer);
+    if (rc) return rc;
+    if ((rc = ensure_work(L->d, S))) return rc;
+    const size_t xb = (size_t)S * L->d.hidden * sizeof(float);
+    const size_t kb = (size_t)S * L->d.topk * sizeof(float);
+    if (ensure_host(xb + 2 * kb)) return -2;
+    memcpy(g.h_stage, x, xb);
+    CZ_CHECK(hipMemcpyAsync(g.work.xin, g.h_stage, xb, hipMemcpyHostToDevice, g.stream), -3);
+    if ((rc = launch_layer(*L, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, nullptr, nullptr, g.stream)))
+        return rc;
+    char *hs = (char *)g.h_stage;
+    CZ_CHECK(hipMemcpyAsync(hs, g.work.out, xb, hipMemcpyDeviceToHost, g.stream), -5);
+    CZ_CHECK(hipMemcpyAsync(hs + xb, g.work.idx, kb, hipMemcpyDeviceToHost, g.stream), -5);
+    CZ_CHECK(hipMemcpyAsync(hs + xb + kb, g.work.gates, kb, hipMemcpyDeviceToHost, g.stream), -5);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    memcpy(out, hs, xb);
+    if (routed_idx) memcpy(routed_idx, hs + xb, kb);
+    if (routed_gates) memcpy(routed_gates, hs + xb + kb, kb);
+    return 0;
+}
+
+static int chain_enqueue(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, float *xn_trace,
+                         uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        int rc = check_layer_ready(L, layer0 + l);
+        if (rc) return rc;
+        if ((rc = ensure_work(L->d, S))) return rc;
+    }
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        const size_t sh = (size_t)S * L->d.hidden, sk = (size_t)S * L->d.topk;
+        const int rc = launch_layer(*L, x_dev, S, x_dev, 1, eps, x_dev, xn_trace ? xn_trace + l * sh : nullptr,
+                                    idx_trace ? idx_trace + l * sk : nullptr,
+                                    gates_trace ? gates_trace + l * sk : nullptr, st);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+extern "C" int colizig_hip_chain_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps,
+                                        float *xn_trace, uint32_t *idx_trace, float *gates_trace, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0) return -1;
+    return chain_enqueue(layer0, nlayers, x_dev, S, eps, xn_trace, idx_trace, gates_trace, pick_stream(stream));
+}
+
+extern "C" int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlayers, float *x_dev, int S,
+                                                  float eps) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0) return -1;
+    // allocate scratch before capture (no allocation inside a capture)
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        int rc = check_layer_ready(L, layer0 + l);
+        if (rc) return rc;
+        if ((rc = ensure_work(L->d, S))) return rc;
+    }
+    CZ_CHECK(hipStreamSynchronize(g.stream), -4);
+    hipGraph_t graph = nullptr;
+    CZ_CHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal), -4);
+    const int rc = chain_enqueue(layer0, nlayers, x_dev, S, eps, nullptr, nullptr, nullptr, g.stream);
+    const hipError_t ec = hipStreamEndCapture(g.stream, &graph);
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (ec != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "hipStreamEndCapture: %s", hipGetErrorString(ec));
+        return -4;
+    }
+    hipGraphExec_t exec = nullptr;
+    if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return -4;
+    }
+    const int64_t h = g.next_handle++;
+    g.graphs[h] = exec;
+    g.graph_defs[h] = graph;
+    return h;
+}
+
+extern "C" int colizig_hip_graph_launch(int64_t handle, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g.graphs.find(handle);
+    if (!g.inited || it == g.graphs.end()) return -1;
+    CZ_CHECK(hipGraphLaunch(it->second, pick_stream(stream)), -4);
+    return 0;
+}
+
+extern "C" void colizig_hip_graph_destroy(int64_t handle) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g.graphs.find(handle);
+    if (it == g.graphs.end()) return;
+    (void)hipStreamSynchronize(g.stream);
+    (void)hipGraphExecDestroy(it->second);
+    g.graphs.erase(it);
+    auto jt = g.graph_defs.find(handle);
+    if (jt != g.graph_defs.end()) {
+        (void)hipGraphDestroy(jt->second);
+        g.graph_defs.erase(jt);
+    }
+}
+
+// ---- synthetic weights -----------------------------------------------------
+__global__ __launch_bounds__(256) void k_synth_fp8_experts(uint8_t *ew, float *es, uint64_t ew_stride,
+                                                           uint64_t es_stride, uint64_t w_off, uint64_t s_off,
+                                                           uint32_t rows, uint32_t cols, uint64_t seed, float stdv) {
+    const uint32_t e = blockIdx.y;
+    uint8_t *w = ew + (uint64_t)e * ew_stride + w_off;
+    float *sc = es + (uint64_t)e * es_stride + s_off;
+    const uint32_t nbc = (cols + CZ_BLOCK - 1) / CZ_BLOCK;
+    const uint32_t br = blockIdx.x / nbc, bc = blockIdx.x - br * nbc;
+    const uint32_t r_lo = br * CZ_BLOCK, c_lo = bc * CZ_BLOCK;
+    const uint32_t nr = min((uint32_t)CZ_BLOCK, rows - r_lo), nc = min((uint32_t)CZ_BLOCK, cols - c_lo);
+    const uint32_t rr = threadIdx.x >> 1, ch = (threadIdx.x & 1) * 64;
+    const uint64_t mseed = cz_mix64(seed ^ cz_mix64(0x5eedull + e));
+    float v[64];
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 64; ++c) {
+        const uint32_t col = ch + c;
+        float val = 0.0f;
+        if (rr < nr && col < nc) val = stdv * cz_normal(mseed, (uint64_t)(r_lo + rr) * cols + (c_lo + col));
+        v[c] = val;
+        amax = fmaxf(amax, fabsf(val));
+    }
+    amax = cz_wave_max(amax);
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+    if (threadIdx.x == 0) sc[blockIdx.x] = scale;
+    if (rr < nr) {
+        uint8_t *row = w + (uint64_t)(r_lo + rr) * cols + c_lo;
+#pragma unroll
+        for (int c = 0; c < 64; c += 2) {
+            float a = fminf(fmaxf(v[c] / scale, -448.0f), 448.0f);
+            float b = fminf(fmaxf(v[c + 1] / scale, -448.0f), 448.0f);
+            const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+            const uint32_t col = ch + c;
+            if (col < nc) row[col] = (uint8_t)(packed & 0xff);
+            if (col + 1 < nc) row[col + 1] = (uint8_t)((packed >> 8) & 0xff);
+        }
+    }
+}
+
+extern "C" int colizig_hip_layer_synth(uint32_t layer, uint64_t seed, float std_w, float std_router) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L) return -1;
+    const colizig_dims &d = L->d;
+    const uint64_t ls = mix64(seed ^ mix64(0xC011716ull + layer));
+    const uint64_t rn = (uint64_t)d.experts * d.hidden;
+    k_synth_f32<<<(uint32_t)std::min<uint64_t>((rn + 255) / 256, 16384), 256, 0, g.stream>>>(L->router, rn,
+                                                                                             mix64(ls + 1), std_router);
+    const uint32_t nbH = nblk(d.hidden), nbI = nblk(d.inter);
+    const uint64_t mb = (uint64_t)d.inter * d.hidden, nsc = (uint64_t)nbI * nbH;
+    // gate, up: [I][H]; down: [H][I]
+    const struct { uint64_t woff, soff; uint32_t rows, cols; } roles[3] = {
+        {0, 0, d.inter, d.hidden}, {mb, nsc, d.inter, d.hidden}, {2 * mb, 2 * nsc, d.hidden, d.inter}};
+    for (int r = 0; r < 3; ++r) {
+        const dim3 grid(nblk(roles[r].rows) * nblk(roles[r].cols), d.experts);
+        k_synth_fp8_experts<<<grid, 256, 0, g.stream>>>(L->ew, L->es, L->ew_stride(), L->es_stride(), roles[r].woff,
+                                                        roles[r].soff, roles[r].rows, roles[r].cols,
+                                                        mix64(ls + 10 + r), std_w);
+    }
+    if (d.shared_inter) {
+        const uint64_t smb = (uint64_t)d.shared_inter * d.hidden, snsc = (uint64_t)nblk(d.shared_inter) * nbH;
+        const struct { uint64_t woff, soff; uint32_t rows, cols; } sroles[3] = {
+            {0, 0, d.shared_inter, d.hidden}, {smb, snsc, d.shared_inter, d.hidden},
+            {2 * smb, 2 * snsc, d.hidden, d.shared_inter}};
+        for (int r = 0; r < 3; ++r) {
+            const dim3 grid(nblk(sroles[r].rows) * nblk(sroles[r].cols), 1);
+            k_synth_fp8_experts<<<grid, 256, 0, g.stream>>>(L->sw, L->ss, 0, 0, sroles[r].woff, sroles[r].soff,
+                                                            sroles[r].rows, sroles[r].cols, mix64(ls + 20 + r),
+                                                            std_w);
+        }
+        k_synth_f32<<<(d.hidden + 255) / 256, 256, 0, g.stream>>>(L->shg, d.hidden, mix64(ls + 30), std_router);
+        L->shared_set = true;
+    }
+    if (hipGetLastError() != hipSuccess) return -4;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    std::fill(L->loaded.begin(), L->loaded.end(), 1);
+    L->nloaded = d.experts;
+    return 0;
+}
+
+extern "C" int colizig_hip_expert_read(uint32_t layer, uint32_t expert, unsigned char *gate_w, float *gate_s,
+                                       unsigned char *up_w, float *up_s, unsigned char *down_w, float *down_s) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || expert >= L->d.experts) return -1;
+    const uint64_t mb = (uint64_t)L->d.inter * L->d.hidden;
+    const uint64_t nsc = (uint64_t)nblk(L->d.inter) * nblk(L->d.hidden);
+    const uint8_t *wb = L->ew + expert * L->ew_stride();
+    const float *sb = L->es + expert * L->es_stride();
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    if (gate_w) CZ_CHECK(hipMemcpy(gate_w, wb, mb, hipMemcpyDeviceToHost), -5);
+    if (up_w) CZ_CHECK(hipMemcpy(up_w, wb + mb, mb, hipMemcpyDeviceToHost), -5);
+    if (down_w) CZ_CHECK(hipMemcpy(down_w, wb + 2 * mb, mb, hipMemcpyDeviceToHost), -5);
+    if (gate_s) CZ_CHECK(hipMemcpy(gate_s, sb, nsc * 4, hipMemcpyDeviceToHost), -5);
+    if (up_s) CZ_CHECK(hipMemcpy(up_s, sb + nsc, nsc * 4, hipMemcpyDeviceToHost), -5);
+    if (down_s) CZ_CHECK(hipMemcpy(down_s, sb + 2 * nsc, nsc * 4, hipMemcpyDeviceToHost), -5);
+    return 0;
+}
+
+extern "C" int colizig_hip_router_read(uint32_t layer, float *router) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || !router) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    CZ_CHECK(hipMemcpy(router, L->router, (size_t)L->d.experts * L->d.hidden * 4, hipMemcpyDeviceToHost), -5);
+    return 0;
+}
+
+extern "C" int colizig_hip_shared_read(uint32_t layer, unsigned char *gate_w, float *gate_s, unsigned char *up_w,
+                                       float *up_s, unsigned char *down_w, float *down_s, float *sh_gate) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || L->d.shared_inter == 0) return -1;
+    const uint64_t mb = (uint64_t)L->d.shared_inter * L->d.hidden;
+    const uint64_t nsc = (uint64_t)nblk(L->d.shared_inter) * nblk(L->d.hidden);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    if (gate_w) CZ_CHECK(hipMemcpy(gate_w, L->sw, mb, hipMemcpyDeviceToHost), -5);
+    if (up_w) CZ_CHECK(hipMemcpy(up_w, L->sw + mb, mb, hipMemcpyDeviceToHost), -5);
+    if (down_w) CZ_CHECK(hipMemcpy(down_w, L->sw + 2 * mb, mb, hipMemcpyDeviceToHost), -5);
+    if (gate_s) CZ_CHECK(hipMemcpy(gate_s, L->ss, nsc * 4, hipMemcpyDeviceToHost), -5);
+    if (up_s) CZ_CHECK(hipMemcpy(up_s, L->ss + nsc, nsc * 4, hipMemcpyDeviceToHost), -5);
+    if (down_s) CZ_CHECK(hipMemcpy(down_s, L->ss + 2 * nsc, nsc * 4, hipMemcpyDeviceToHost), -5);
+    if (sh_gate) CZ_CHECK(hipMemcpy(sh_gate, L->shg, (size_t)L->d.hidden * 4, hipMemcpyDeviceToHost), -5);
+    return 0;
+}
+
+// ---- per-kernel timing pass --------------------------------------------------
+extern "C" int colizig_hip_chain_profile(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps,
+                                         int steps, float *ms_out) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || steps < 1 || !ms_out) return -1;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        int rc = check_layer_ready(L, layer0 + l);
+        if (rc) return rc;
+        if ((rc = ensure_work(L->d, S))) return rc;
+    }
+    std::vector<hipEvent_t> ev(6ull * nlayers);
+    for (auto &e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return -2;
+    double sum[3] = {0, 0, 0};
+    int rc = 0;
+    for (int t = 0; t < steps && rc == 0; ++t) {
+        for (uint32_t l = 0; l < nlayers && rc == 0; ++l) {
+            LayerHost *L = find_layer(layer0 + l);
+            rc = launch_layer(*L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, g.stream, &ev[6ull * l]);
+        }
+        if (rc) break;
+        if (hipStreamSynchronize(g.stream) != hipSuccess) { rc = -5; break; }
+        for (uint32_t l = 0; l < nlayers; ++l)
+            for (int k = 0; k < 3; ++k) {
+                float ms = 0.0f;
+                if (hipEventElapsedTime(&ms, ev[6ull * l + 2 * k], ev[6ull * l + 2 * k + 1]) != hipSuccess) rc = -5;
+                sum[k] += ms;
+            }
+    }
+    for (auto &e : ev) (void)hipEventDestroy(e);
+    if (rc) return rc;
+    for (int k = 0; k < 3; ++k) ms_out[k] = (float)(sum[k] / ((double)steps * nlayers));
+    return 0;
+}
+
+extern "C" int colizig_hip_expert_slab_read(uint32_t layer, unsigned char *ew, float *es) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || !ew || !es) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    CZ_CHECK(hipMemcpy(ew, L->ew, L->ew_stride() * L->d.experts, hipMemcpyDeviceToHost), -5);
+    CZ_CHECK(hipMemcpy(es, L->es, L->es_stride() * L->d.experts * sizeof(float), hipMemcpyDeviceToHost), -5);
+    return 0;
+}
+
+// ---- exp test hooks -------------------------------------------------------------
+__global__ void k_expf(const float *in, float *out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = cz_expf(in[i]);
+}
+
+extern "C" int colizig_hip_expf_dev(const float *in, float *out, int n) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || n < 1 || !in || !out) return -1;
+    float *di = nullptr, *dout = nullptr;
+    int rc = 0;
+    if (hipMalloc(&di, (size_t)n * 4) != hipSuccess || hipMalloc(&dout, (size_t)n * 4) != hipSuccess) {
+        rc = -2;
+    } else if (hipMemcpy(di, in, (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        rc = -3;
+    } else {
+        k_expf<<<(n + 255) / 256, 256, 0, g.stream>>>(di, dout, n);
+        if (hipGetLastError() != hipSuccess) rc = -4;
+        else if (hipStreamSynchronize(g.stream) != hipSuccess ||
+                 hipMemcpy(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            rc = -5;
+    }
+    if (di) (void)hipFree(di);
+    if (dout) (void)hipFree(dout);
+    return rc;
+}
+
+extern "C" float colizig_hip_expf_host(float x) { return cz_expf(x); }
+
+// ---- device memory / stream / event helpers -------------------------------------
+extern "C" void *colizig_hip_malloc(uint64_t bytes) {
+    CsrGuard csr;
+    void *p = nullptr;
+    if (!g.inited || bytes == 0 || hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    return p;
+}
+extern "C" void colizig_hip_free(void *p) {
+    CsrGuard csr;
+    if (g.inited && p) (void)hipFree(p);
+}
+extern "C" int colizig_hip_memcpy_htod(void *dst, const void *src, uint64_t bytes) {
+    CsrGuard csr;
+    if (!g.inited) return -1;
+    CZ_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    return 0;
+}
+extern "C" int colizig_hip_memcpy_dtoh(void *dst, const void *src, uint64_t bytes) {
+    CsrGuard csr;
+    if (!g.inited) return -1;
+    CZ_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.stream), -5);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    return 0;
+}
+extern "C" int colizig_hip_memset(void *dst, int value, uint64_t bytes) {
+    CsrGuard csr;
+    if (!g.inited) return -1;
+    CZ_CHECK(hipMemsetAsync(dst, value, bytes, g.stream), -4);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -4);
+    return 0;
+}
+extern "C" void *colizig_hip_stream(void) { return g.inited ? (void *)g.stream : nullptr; }
+extern "C" int colizig_hip_sync(void) {
+    CsrGuard csr;
+    if (!g.inited) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    return 0;
+}
+extern "C" int64_t colizig_hip_event_create(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited) return -1;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -2;
+    const int64_t h = g.next_handle++;
+    g.events[h] = e;
+    return h;
+}
+extern "C" int colizig_hip_event_record(int64_t ev, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g.events.find(ev);
+    if (!g.inited || it == g.events.end()) return -1;
+    CZ_CHECK(hipEventRecord(it->second, pick_stream(stream)), -4);
+    return 0;
+}
+extern "C" float colizig_hip_event_elapsed_ms(int64_t a, int64_t b) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto ia = g.events.find(a), ib = g.events.find(b);
+    if (!g.inited || ia == g.events.end() || ib == g.events.end()) return -1.0f;
+    if (hipEventSynchronize(ib->second) != hipSuccess) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, ia->second, ib->second) != hipSuccess) return -1.0f;
+    return ms;
+}
+extern "C" void colizig_hip_event_destroy(int64_t ev) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g.events.find(ev);
+    if (it == g.events.end()) return;
+    (void)hipEventDestroy(it->second);
+    g.events.erase(it);
+}
+extern "C" const char *colizig_hip_last_error(void) { return g_err; }

@@ -1,0 +1,105 @@
+// cz_device.h - device helpers for the gfx950 MoE expert path: f32 exp,
+// sigmoid/SiLU, OCP E4M3 decode, wave64 reductions.
+//
+// Everything here is compiled with -ffp-contract=off: a fused multiply-add
+// appears only where it is written (__builtin_fmaf / __builtin_fma).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define CZ_BLOCK 128
+#define CZ_WAVE 64
+
+typedef float cz_float2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// f32 exp: the f32 rounding of a double-precision evaluation
+//   k = nearest integer to x/ln2 (shifter 0x1.8p52, two separate roundings)
+//   r = (x - k*ln2_hi) - k*ln2_lo via two fma
+//   p = sum_{n<=13} r^n/n! by Horner with fma  (|r| <= ln2/2, truncation < 2^-57)
+//   exp(x) ~= p * 2^k, exact power-of-two scaling, then one RNE to f32.
+// Every step is an IEEE-754 double add/mul/fma or an exact conversion, so the
+// host and the GPU produce the same bits.  Exhaustively (all 2^32 inputs) it
+// equals the correctly rounded f32 exp.  Used by the router softmax
+// (moe.zig:443) and the sigmoid in SiLU (activation.zig:9-20).
+// ---------------------------------------------------------------------------
+__host__ __device__ inline float cz_expf(float xf) {
+    if (xf != xf) return xf + xf;
+    double x = (double)xf;
+    x = x > 100.0 ? 100.0 : x;    // exp(100) rounds to +inf in f32
+    x = x < -120.0 ? -120.0 : x;  // exp(-120) rounds to +0 in f32
+    const double t0 = x * 0x1.71547652b82fep+0;  // 1/ln2
+    const double t1 = t0 + 0x1.8p52;
+    const double kd = t1 - 0x1.8p52;
+    double r = __builtin_fma(-kd, 0x1.62e42fefa39efp-1, x);  // ln2 high part
+    r = __builtin_fma(-kd, 0x1.abc9e3b39803fp-56, r);         // ln2 low part
+    double p = 0x1.6124613a86d09p-33;                         // 1/13!
+    p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);           // 1/12!
+    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);           // 1/11!
+    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);           // 1/10!
+    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);           // 1/9!
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);           // 1/8!
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);           // 1/7!
+    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);           // 1/6!
+    p = __builtin_fma(p, r, 0x1.1111111111111p-7);            // 1/5!
+    p = __builtin_fma(p, r, 0x1.5555555555555p-5);            // 1/4!
+    p = __builtin_fma(p, r, 0x1.5555555555555p-3);            // 1/3!
+    p = __builtin_fma(p, r, 0x1.0p-1);                        // 1/2!
+    p = __builtin_fma(p, r, 1.0);                             // 1/1!
+    p = __builtin_fma(p, r, 1.0);                             // 1/0!
+    const int k = (int)kd;
+    const uint64_t sbits = (uint64_t)(int64_t)(k + 1023) << 52;
+    const double scale = __builtin_bit_cast(double, sbits);
+    return (float)(p * scale);
+}
+
+// activation.zig:9-16: two-branch stable sigmoid, f32 arithmetic.
+__host__ __device__ inline float cz_sigmoid(float x) {
+    if (x >= 0.0f) {
+        const float z = cz_expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    const float z = cz_expf(x);
+    return z / (1.0f + z);
+}
+
+// activation.zig:18-20
+__host__ __device__ inline float cz_silu(float x) { return x * cz_sigmoid(x); }
+
+// ---------------------------------------------------------------------------
+// OCP E4M3 (e4m3fn) decode with gfx950's v_cvt_pk_f32_fp8: two bytes of a
+// dword per instruction, exact (every E4M3 value is an f32).  The dequantised
+// weight is then ONE f32 multiply by the 128x128 block scale, the definition
+// fp8.zig:105 uses.
+// ---------------------------------------------------------------------------
+__device__ inline cz_float2 cz_fp8x2_lo(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false); }
+__device__ inline cz_float2 cz_fp8x2_hi(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true); }
+
+// acc += x[0..3] * (e4m3(bytes of w) * s), element order = byte order.
+__device__ inline float cz_dot4_fp8(uint32_t w, float s, const float *x4, float acc) {
+    const cz_float2 lo = cz_fp8x2_lo(w);
+    const cz_float2 hi = cz_fp8x2_hi(w);
+    acc = __builtin_fmaf(x4[0], lo.x * s, acc);
+    acc = __builtin_fmaf(x4[1], lo.y * s, acc);
+    acc = __builtin_fmaf(x4[2], hi.x * s, acc);
+    acc = __builtin_fmaf(x4[3], hi.y * s, acc);
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ inline float cz_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, CZ_WAVE);
+    return v;
+}
+
+__device__ inline float cz_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, CZ_WAVE));
+    return v;
+}
+
+__device__ inline uint32_t cz_lane() { return threadIdx.x & (CZ_WAVE - 1); }

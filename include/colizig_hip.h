@@ -1,0 +1,194 @@
+/*
+ * colizig_hip.h - C-ABI of libcolizig_hip.so, the MI355X (gfx950) block-FP8
+ * MoE expert path for colizig.
+ *
+ * Plain C types only (pointers, sizes, ints).  Two groups of entry points:
+ *
+ *  1. The six symbols colizig's engine already resolves by name
+ *     (src/backend/gpu.zig:84-89) with the exact signatures of its extern fn
+ *     types (src/backend/gpu.zig:20-34), replacing the CUDA DLL
+ *     (src/backend/cuda/colizig_cuda.cu:171-284).  Same return codes, same
+ *     ownership (caller-owned host pointers valid for the call), same
+ *     MXCSR save/restore at every entry.
+ *
+ *  2. Optional MoE-level extensions (colizig_hip_*).  A loader that finds any
+ *     of them missing keeps using group 1 only, the loader's existing rule
+ *     (gpu.zig:84-89).  Same error convention: 0 ok, negative = the caller
+ *     falls back to its CPU path.
+ *
+ * Not thread-safe across calls on one process (one global context, as the
+ * CUDA DLL): the caller serialises, as gpu.zig:55-62 does.
+ */
+#ifndef COLIZIG_HIP_H
+#define COLIZIG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* 1. the existing backend ABI                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces colizig_cuda.cu:171-187 (InitFn, gpu.zig:20).  Idempotent.
+ * 0 ok; -1 no device; -2 set-device failed; -3 device query failed;
+ * -4 device constant setup failed. */
+int colizig_cuda_init(void);
+
+/* Replaces colizig_cuda.cu:189-191 (NameFn, gpu.zig:22).  "" before init;
+ * library-owned static buffer. */
+const char *colizig_cuda_device_name(void);
+
+/* Replaces colizig_cuda.cu:195-202 (SetBudgetFn, gpu.zig:23).  Bytes of HBM
+ * the keyed weight cache may hold; 0 disables it.  Clamped to
+ * free - free/8.  No-op before init. */
+void colizig_cuda_set_vram_budget(uint64_t bytes);
+
+/* Replaces colizig_cuda.cu:204-209 (StatsFn, gpu.zig:24).  NULL-tolerant. */
+void colizig_cuda_stats(uint64_t *hits, uint64_t *misses, uint64_t *uploaded_mib, uint64_t *resident);
+
+/* Replaces colizig_cuda.cu:211-224 (ShutdownFn, gpu.zig:21).  Frees every
+ * device allocation (also the MoE layers below) and resets the context;
+ * safe when not initialised. */
+void colizig_cuda_shutdown(void);
+
+/* Replaces colizig_cuda.cu:228-284 (MatmulFp8Fn, gpu.zig:25-34), called from
+ * src/ops/fp8.zig:182.  Synchronous:
+ *   y[S,O] = x[S,I] @ (e4m3(w[O,I]) * scales[o/128, i/128])^T
+ * w row-major [O,I] E4M3 (OCP e4m3fn), scales row-major
+ * [ceil(O/128), ceil(I/128)] f32.  key 0 = upload w every call; non-zero =
+ * keep w in the HBM cache under that key (fp8 key scheme moe.zig:97-99).
+ * 0 ok; -1 bad args / not initialised; -2 device alloc; -3 H2D copy;
+ * -4 launch; -5 D2H copy / kernel fault. */
+int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, const float *scales, int S, int I,
+                            int O, uint64_t key);
+
+/* ------------------------------------------------------------------------ */
+/* 2. MoE-level extensions                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Mirrors src/qwen38/moe.zig:23-46 `Dims` (shape contract of one layer). */
+typedef struct colizig_dims {
+    uint32_t hidden;       /* H */
+    uint32_t experts;      /* E */
+    uint32_t topk;         /* K */
+    uint32_t inter;        /* I, routed moe_intermediate */
+    uint32_t shared_inter; /* SI, 0 = no shared expert */
+    uint32_t norm_topk;    /* renormalise gates over the top-k */
+} colizig_dims;
+
+/* Bit-exact dequantisation hook (fp8.zig:123-130 semantics: one f32
+ * multiply e4m3(b) * scale, the same arithmetic the GEMV kernels use in
+ * registers).  Host pointers: out[rows*cols] f32, w[rows*cols] E4M3,
+ * scales[ceil(rows/128)*ceil(cols/128)].  No counterpart in the reference:
+ * it exists so the dequantised weights can be compared bit for bit. */
+int colizig_hip_dequant_fp8(float *out, const unsigned char *w, const float *scales, int rows, int cols);
+
+/* Registers one MoE layer: replaces Layer.load (moe.zig:306-328).
+ * router[E*H] f32 (the reference's `gate.weight`, moe.zig:316) is copied
+ * into HBM.  Re-registering a layer frees its previous weights.  Experts
+ * start absent; forward fails with -6 until every expert is loaded. */
+int colizig_hip_layer_init(uint32_t layer, const colizig_dims *dims, const float *router);
+
+/* Copies expert `expert` of `layer` into its HBM slot: replaces loadExpert
+ * (moe.zig:251-292) + ExpertCache.fill (moe.zig:199-217).  gate/up are
+ * [I,H] E4M3 with [ceil(I/128), ceil(H/128)] scales, down is [H,I] with
+ * [ceil(H/128), ceil(I/128)] scales. */
+int colizig_hip_expert_load(uint32_t layer, uint32_t expert, const unsigned char *gate_w, const float *gate_s,
+                            const unsigned char *up_w, const float *up_s, const unsigned char *down_w,
+                            const float *down_s);
+
+/* Shared expert of a layer (moe.zig:300-303, 319-325), block-FP8:
+ * gate/up [SI,H], down [H,SI], sh_gate[H] f32 (shared_expert_gate.weight). */
+int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char *gate_w, const float *gate_s,
+                                 const unsigned char *up_w, const float *up_s, const unsigned char *down_w,
+                                 const float *down_s, const float *sh_gate);
+
+/* moe.forward (moe.zig:409-426) on host pointers, synchronous:
+ * out[S*H] = MoE(x[S*H]).  routed_idx[S*K] / routed_gates[S*K] (nullable)
+ * receive each token's top-k expert ids and gates in selection order.
+ * 0 ok; -1 bad args; -2 alloc; -3 H2D; -4 launch; -5 D2H/fault;
+ * -6 layer not registered or experts missing. */
+int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, uint32_t *routed_idx,
+                            float *routed_gates);
+
+/* Same on device pointers, asynchronous on `stream` (a hipStream_t; NULL =
+ * the library's stream).  Pointers must stay valid until the stream
+ * reaches the end of this work. */
+int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, int S, float *out_dev, uint32_t *idx_dev,
+                                float *gates_dev, void *stream);
+
+/* Decode chain over layers [layer0, layer0+nlayers) on device memory:
+ *   x <- x + MoE_l(rmsnorm(x)),  rmsnorm(x)_i = x_i / sqrt(mean(x^2) + eps)
+ * (unit-weight RMSNorm; the residual stream the MoE blocks sit in,
+ * qwen3moe/model.zig:228-231).  x_dev[S*H] is updated in place.  Optional
+ * per-layer traces (device pointers, NULL = off): xn_trace[nlayers*S*H] the
+ * router inputs, idx_trace/gates_trace[nlayers*S*K] the routing.
+ * Asynchronous on `stream` (NULL = library stream). */
+int colizig_hip_chain_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, float *xn_trace,
+                             uint32_t *idx_trace, float *gates_trace, void *stream);
+
+/* Captures colizig_hip_chain_decode (traces off) into a HIP graph and
+ * returns a handle (>0) for colizig_hip_graph_launch; <0 on error. */
+int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps);
+int colizig_hip_graph_launch(int64_t handle, void *stream);
+void colizig_hip_graph_destroy(int64_t handle);
+
+/* Timing pass: runs the chain eagerly `steps` times with HIP events around
+ * each kernel on the library stream; ms_out[3] receives the mean duration
+ * (ms) of the router, gate/up and down kernels per layer.  x_dev advances as
+ * in colizig_hip_chain_decode. */
+int colizig_hip_chain_profile(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, int steps,
+                              float *ms_out);
+
+/* Fills a registered layer (router, every expert, shared expert) with
+ * seeded synthetic weights directly in HBM: router and sh_gate f32
+ * N(0, std_router); expert matrices N(0, std_w) quantised per 128x128 block
+ * to E4M3 (RNE, saturating) with scale = amax/448 (1 for an all-zero
+ * block).  A workload generator for benchmarks and tests, no counterpart in
+ * the reference (its fixtures come from tools/gen_tiny_fixture.zig). */
+int colizig_hip_layer_synth(uint32_t layer, uint64_t seed, float std_w, float std_router);
+
+/* Copies a registered expert / the router / the shared expert back to host
+ * memory (same layouts as the load calls); for checking and baselines. */
+int colizig_hip_expert_read(uint32_t layer, uint32_t expert, unsigned char *gate_w, float *gate_s,
+                            unsigned char *up_w, float *up_s, unsigned char *down_w, float *down_s);
+int colizig_hip_router_read(uint32_t layer, float *router);
+/* The whole expert slab of a layer in its HBM layout: ew[E * 3*I*H] bytes
+ * (expert e: gate | up | down) and es[E * 3*nblk(I)*nblk(H)] scales. */
+int colizig_hip_expert_slab_read(uint32_t layer, unsigned char *ew, float *es);
+int colizig_hip_shared_read(uint32_t layer, unsigned char *gate_w, float *gate_s, unsigned char *up_w,
+                            float *up_s, unsigned char *down_w, float *down_s, float *sh_gate);
+
+/* Device-side f32 exp used by the router softmax and SiLU, evaluated on the
+ * GPU for n inputs (host pointers); and the same function run on the host.
+ * Test hooks for the router's bit-exactness. */
+int colizig_hip_expf_dev(const float *in, float *out, int n);
+float colizig_hip_expf_host(float x);
+
+/* Small device-memory / stream / event helpers so callers without a GPU
+ * framework can drive the *_dev entry points. */
+void *colizig_hip_malloc(uint64_t bytes);
+void colizig_hip_free(void *p);
+int colizig_hip_memcpy_htod(void *dst, const void *src, uint64_t bytes);
+int colizig_hip_memcpy_dtoh(void *dst, const void *src, uint64_t bytes);
+int colizig_hip_memset(void *dst, int value, uint64_t bytes);
+void *colizig_hip_stream(void); /* the library's stream */
+int colizig_hip_sync(void);     /* synchronise the library's stream */
+/* Events on the library stream: create returns a handle; record puts it on
+ * `stream` (NULL = library stream); elapsed_ms waits for `b`. */
+int64_t colizig_hip_event_create(void);
+int colizig_hip_event_record(int64_t ev, void *stream);
+float colizig_hip_event_elapsed_ms(int64_t a, int64_t b);
+void colizig_hip_event_destroy(int64_t ev);
+
+/* Last error message of the library (static buffer). */
+const char *colizig_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
