@@ -118,12 +118,13 @@ def main():
     tok_s = 1000.0 / ms_per_step
     log(f"timed: {args.steps} steps, {ms_per_step * 1000:.1f} us/token, {tok_s:.1f} tok/s (wall {wall:.3f}s)")
 
-    # per-kernel durations (HIP events around each kernel, eager launches)
-    ms3 = (ctypes.c_float * 3)()
-    rc = hip.colizig_hip_chain_profile(0, NL, xb.ptr, 1, eps, args.profile_steps, ms3)
+    # per-kernel durations: each kernel kind replayed alone in a HIP graph over
+    # the layers, between two events on the library stream
+    us3 = (ctypes.c_float * 3)()
+    rc = hip.colizig_hip_chain_kernel_times(0, NL, xb.ptr, 1, eps, args.profile_steps, us3)
     if rc != 0:
-        raise RuntimeError(f"profile pass failed: {_lib.last_error()}")
-    router_us, up_us, down_us = (ms3[i] * 1000.0 for i in range(3))
+        raise RuntimeError(f"kernel timing pass failed: {_lib.last_error()}")
+    router_us, up_us, down_us = (float(us3[i]) for i in range(3))
     b = per_token_bytes(c)
     up_gbs = b["up"] / (up_us * 1e-6) / 1e9
     down_gbs = b["down"] / (down_us * 1e-6) / 1e9
@@ -159,7 +160,7 @@ def main():
         "hbm_gbs_per_token": round(tok_bytes * tok_s / 1e9, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_up_fast (gate/up GEMV + SiLU, 8 experts)",
+            "kernel": "k_up_fast (top-k + gate/up GEMV + SiLU, 8 experts)",
             "achieved": round(up_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

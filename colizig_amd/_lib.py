@@ -59,8 +59,8 @@ SIGNATURES = {
                                                         ctypes.c_float]),
     "colizig_hip_graph_launch": (ctypes.c_int, [ctypes.c_int64, vp]),
     "colizig_hip_graph_destroy": (None, [ctypes.c_int64]),
-    "colizig_hip_chain_profile": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,
-                                                 ctypes.c_float, ctypes.c_int, vp]),
+    "colizig_hip_chain_kernel_times": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,
+                                                      ctypes.c_float, ctypes.c_int, vp]),
     "colizig_hip_expert_slab_read": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
     "colizig_hip_layer_synth": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
     "colizig_hip_expert_read": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp]),

@@ -85,9 +85,9 @@ struct LayerHost {
 struct Work {
     float *xin = nullptr, *out = nullptr, *xn = nullptr, *logits = nullptr, *gates = nullptr, *sgate = nullptr;
     float *h = nullptr, *hs = nullptr;
-    uint32_t *idx = nullptr, *counters = nullptr;
+    uint32_t *idx = nullptr;
     size_t cap_xin = 0, cap_out = 0, cap_xn = 0, cap_logits = 0, cap_idx = 0, cap_gates = 0, cap_sgate = 0,
-           cap_cnt = 0, cap_h = 0, cap_hs = 0;
+           cap_h = 0, cap_hs = 0;
 };
 
 struct Ctx {
@@ -156,14 +156,13 @@ int ensure_host(size_t need) {
 }
 
 template <typename T>
-int grow(T **p, size_t *cap, size_t need, bool zero) {
+int grow(T **p, size_t *cap, size_t need) {
     if (*cap >= need) return 0;
     if (*p) g.retired.push_back((void *)*p);
     *p = nullptr;
     *cap = 0;
     void *q = nullptr;
     if (hipMalloc(&q, need * sizeof(T)) != hipSuccess) return -1;
-    if (zero && hipMemset(q, 0, need * sizeof(T)) != hipSuccess) return -1;
     *p = (T *)q;
     *cap = need;
     return 0;
@@ -173,13 +172,11 @@ int grow(T **p, size_t *cap, size_t need, bool zero) {
 int ensure_work(const colizig_dims &d, int S) {
     Work &w = g.work;
     const size_t s = (size_t)S;
-    const size_t tiles = s;  // router token tiles are at least one token wide
-    if (grow(&w.xin, &w.cap_xin, s * d.hidden, false) || grow(&w.out, &w.cap_out, s * d.hidden, false) ||
-        grow(&w.xn, &w.cap_xn, s * d.hidden, false) || grow(&w.logits, &w.cap_logits, s * d.experts, false) ||
-        grow(&w.idx, &w.cap_idx, s * d.topk, false) || grow(&w.gates, &w.cap_gates, s * d.topk, false) ||
-        grow(&w.sgate, &w.cap_sgate, s, false) || grow(&w.counters, &w.cap_cnt, tiles, true) ||
-        grow(&w.h, &w.cap_h, s * d.topk * (size_t)d.inter, false) ||
-        grow(&w.hs, &w.cap_hs, std::max<size_t>(1, s * d.shared_inter), false)) {
+    if (grow(&w.xin, &w.cap_xin, s * d.hidden) || grow(&w.out, &w.cap_out, s * d.hidden) ||
+        grow(&w.xn, &w.cap_xn, s * d.hidden) || grow(&w.logits, &w.cap_logits, s * d.experts) ||
+        grow(&w.idx, &w.cap_idx, s * d.topk) || grow(&w.gates, &w.cap_gates, s * d.topk) ||
+        grow(&w.sgate, &w.cap_sgate, s) || grow(&w.h, &w.cap_h, s * d.topk * (size_t)d.inter) ||
+        grow(&w.hs, &w.cap_hs, std::max<size_t>(1, s * d.shared_inter))) {
         snprintf(g_err, sizeof g_err, "scratch allocation failed (S=%d)", S);
         return -2;
     }
@@ -200,108 +197,128 @@ int router_tokens_per_tile(uint32_t H) {
     return (int)std::min<uint32_t>(CZ_ROUTER_TT, std::max<uint32_t>(1u, 8192u / std::max<uint32_t>(H, 1u)));
 }
 
+constexpr int kUpRows = 2;    // rows of each of gate/up per wave
+constexpr int kDownKC = 8;    // experts per load batch of the down kernel
+
+enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
+
+void launch_router(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);
+    const size_t lds = (size_t)A.tt * L.H * sizeof(float);
+    switch ((L.H % 32) ? 0u : L.H / 32) {
+        case 8: k_router_fast<8><<<grid, 64, lds, st>>>(A); return;
+        case 16: k_router_fast<16><<<grid, 64, lds, st>>>(A); return;
+        case 32: k_router_fast<32><<<grid, 64, lds, st>>>(A); return;
+        case 64: k_router_fast<64><<<grid, 64, lds, st>>>(A); return;
+        case 96: k_router_fast<96><<<grid, 64, lds, st>>>(A); return;
+        case 128: k_router_fast<128><<<grid, 64, lds, st>>>(A); return;
+        default: k_router_generic<<<grid, 64, lds, st>>>(A); return;
+    }
+}
+
 template <int NB>
-void launch_up(const LayerDev &L, const float *xn, const uint32_t *idx, float *h, float *hs, int S, hipStream_t st) {
-    constexpr int RW = 2;
-    const uint32_t rows_wg = 4 * RW;
-    const uint32_t blocks = (uint32_t)S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
-                            (L.SI ? (uint32_t)S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
-    k_up_fast<NB, RW><<<blocks, 256, 0, st>>>(L, xn, idx, h, hs, S);
+void launch_up_t(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    const uint32_t rows_wg = 4 * kUpRows;
+    const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
+                            (L.SI ? (uint32_t)A.S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
+    k_up_fast<NB, kUpRows><<<blocks, 256, 0, st>>>(A);
+}
+
+void launch_up(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    switch ((L.H % 64) ? 0u : L.H / 64) {
+        case 4: launch_up_t<4>(A, st); return;
+        case 8: launch_up_t<8>(A, st); return;
+        case 16: launch_up_t<16>(A, st); return;
+        case 32: launch_up_t<32>(A, st); return;
+        case 48: launch_up_t<48>(A, st); return;
+        case 64: launch_up_t<64>(A, st); return;
+        default: {
+            const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)A.S * ((L.SI + 3) / 4) : 0u);
+            k_up_generic<<<blocks, 256, 0, st>>>(A);
+            return;
+        }
+    }
 }
 
 template <int NBI, int NBS>
-void launch_down(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
-                 const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
-    constexpr int RD = 2;
-    const uint32_t rows_wg = 4 * RD;
-    const uint32_t blocks = (uint32_t)S * ((L.H + rows_wg - 1) / rows_wg);
-    k_down_fast<NBI, NBS, RD><<<blocks, 256, 0, st>>>(L, h, hs, idx, gates, sgate, xres, out, S);
-}
-
-bool up_fast(const LayerDev &L, const float *xn, const uint32_t *idx, float *h, float *hs, int S, hipStream_t st) {
-    if (L.H % 64) return false;
-    switch (L.H / 64) {
-        case 4: launch_up<4>(L, xn, idx, h, hs, S, st); return true;
-        case 8: launch_up<8>(L, xn, idx, h, hs, S, st); return true;
-        case 16: launch_up<16>(L, xn, idx, h, hs, S, st); return true;
-        case 32: launch_up<32>(L, xn, idx, h, hs, S, st); return true;
-        case 48: launch_up<48>(L, xn, idx, h, hs, S, st); return true;
-        case 64: launch_up<64>(L, xn, idx, h, hs, S, st); return true;
-        default: return false;
-    }
+void launch_down_t(const StepArgs &A, hipStream_t st) {
+    const uint32_t blocks = (uint32_t)A.S * ((A.L.H + 3) / 4);
+    k_down_fast<NBI, NBS, kDownKC><<<blocks, 256, 0, st>>>(A);
 }
 
 template <int NBI>
-bool down_fast_s(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
-                 const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
-    if (L.SI == 0) { launch_down<NBI, 0>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true; }
-    if (L.SI % 64) return false;
-    switch (L.SI / 64) {
-        case 8: launch_down<NBI, 8>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
-        case 16: launch_down<NBI, 16>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
-        case 32: launch_down<NBI, 32>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
-        case 64: launch_down<NBI, 64>(L, h, hs, idx, gates, sgate, xres, out, S, st); return true;
+bool launch_down_s(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    if (L.SI == 0) { launch_down_t<NBI, 0>(A, st); return true; }
+    switch ((L.SI % 64) ? 0u : L.SI / 64) {
+        case 8: launch_down_t<NBI, 8>(A, st); return true;
+        case 16: launch_down_t<NBI, 16>(A, st); return true;
+        case 32: launch_down_t<NBI, 32>(A, st); return true;
+        case 64: launch_down_t<NBI, 64>(A, st); return true;
         default: return false;
     }
 }
 
-bool down_fast(const LayerDev &L, const float *h, const float *hs, const uint32_t *idx, const float *gates,
-               const float *sgate, const float *xres, float *out, int S, hipStream_t st) {
-    if (L.I % 64) return false;
-    switch (L.I / 64) {
-        case 4: return down_fast_s<4>(L, h, hs, idx, gates, sgate, xres, out, S, st);
-        case 8: return down_fast_s<8>(L, h, hs, idx, gates, sgate, xres, out, S, st);
-        case 12: return down_fast_s<12>(L, h, hs, idx, gates, sgate, xres, out, S, st);
-        case 16: return down_fast_s<16>(L, h, hs, idx, gates, sgate, xres, out, S, st);
-        default: return false;
+void launch_down(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    bool ok = false;
+    switch ((L.I % 64) ? 0u : L.I / 64) {
+        case 4: ok = launch_down_s<4>(A, st); break;
+        case 8: ok = launch_down_s<8>(A, st); break;
+        case 12: ok = launch_down_s<12>(A, st); break;
+        case 16: ok = launch_down_s<16>(A, st); break;
+        default: break;
+    }
+    if (!ok) {
+        const uint32_t blocks = (uint32_t)A.S * ((L.H + 3) / 4);
+        k_down_generic<<<blocks, 256, 0, st>>>(A);
     }
 }
 
 // x: router input (rms=0) or residual (rms=1); out may alias xres.
-// ev (nullable): six events recorded before/after the router, up and down
-// kernels, for the per-kernel timing pass.
-int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
-                 float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st,
-                 hipEvent_t *ev = nullptr) {
-    const LayerDev L = Lh.dev();
+StepArgs step_args(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                   float *xn_trace, uint32_t *idx_trace, float *gates_trace) {
     Work &w = g.work;
-    RouterArgs A{};
-    A.L = L;
+    StepArgs A{};
+    A.L = Lh.dev();
     A.x = x;
     A.xn = w.xn;
     A.logits = w.logits;
     A.idx = w.idx;
     A.gates = w.gates;
     A.sgate = w.sgate;
-    A.counters = w.counters;
+    A.h = w.h;
+    A.hs = w.hs;
+    A.xres = xres;
+    A.out = out;
     A.idx_trace = idx_trace;
     A.gates_trace = gates_trace;
     A.xn_trace = xn_trace;
     A.S = S;
+    A.tt = router_tokens_per_tile(Lh.d.hidden);
     A.rms = rms;
     A.eps = eps;
-    const int tt = router_tokens_per_tile(L.H);
-    A.tt = tt;
-    const dim3 rgrid((L.E + 7) / 8, (S + tt - 1) / tt);
-    const size_t lds = std::max<size_t>((size_t)tt * L.H, 4 * CZ_MAX_E) * sizeof(float);
-    if (ev) (void)hipEventRecord(ev[0], st);
-    k_router<<<rgrid, 256, lds, st>>>(A);
-    if (ev) (void)hipEventRecord(ev[1], st);
-    const float *xn = rms ? w.xn : x;
-    if (ev) (void)hipEventRecord(ev[2], st);
-    if (!up_fast(L, xn, w.idx, w.h, w.hs, S, st)) {
-        const uint32_t blocks = (uint32_t)S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)S * ((L.SI + 3) / 4) : 0u);
-        k_up_generic<<<blocks, 256, 0, st>>>(L, xn, w.idx, w.h, w.hs, S);
+    return A;
+}
+
+int launch_step(const StepArgs &A, hipStream_t st, int which = kAll) {
+    if (which & kRouter) launch_router(A, st);
+    if (which & kUp) launch_up(A, st);
+    if (which & kDown) launch_down(A, st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "kernel launch: %s", hipGetErrorString(e));
+        return -4;
     }
-    if (ev) (void)hipEventRecord(ev[3], st);
-    if (ev) (void)hipEventRecord(ev[4], st);
-    if (!down_fast(L, w.h, w.hs, w.idx, w.gates, w.sgate, xres, out, S, st)) {
-        const uint32_t blocks = (uint32_t)S * ((L.H + 3) / 4);
-        k_down_generic<<<blocks, 256, 0, st>>>(L, w.h, w.hs, w.idx, w.gates, w.sgate, xres, out, S);
-    }
-    if (ev) (void)hipEventRecord(ev[5], st);
-    if (hipGetLastError() != hipSuccess) return -4;
     return 0;
+}
+
+int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                 float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+    return launch_step(step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace), st);
 }
 
 LayerHost *find_layer(uint32_t layer) {
@@ -403,7 +420,7 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (g.h_stage) (void)hipHostFree(g.h_stage);
     Work &w = g.work;
     for (void *p : {(void *)w.xin, (void *)w.out, (void *)w.xn, (void *)w.logits, (void *)w.gates,
-                    (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx, (void *)w.counters})
+                    (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     (void)hipStreamDestroy(g.stream);
@@ -894,40 +911,63 @@ extern "C" int colizig_hip_shared_read(uint32_t layer, unsigned char *gate_w, fl
 }
 
 // ---- per-kernel timing pass --------------------------------------------------
-extern "C" int colizig_hip_chain_profile(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps,
-                                         int steps, float *ms_out) {
+// One eager chain step leaves valid routing/scratch state; then, per kernel
+// kind, a HIP graph of `reps` passes over the layers launching only that
+// kernel (same arguments as in the chain; the down kernel writes to scratch so
+// x is left as the chain step made it) is replayed between two events.
+extern "C" int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps,
+                                              int reps, float *us_out) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || steps < 1 || !ms_out) return -1;
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || reps < 1 || !us_out) return -1;
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
         if ((rc = ensure_work(L->d, S))) return rc;
     }
-    std::vector<hipEvent_t> ev(6ull * nlayers);
-    for (auto &e : ev)
-        if (hipEventCreate(&e) != hipSuccess) return -2;
-    double sum[3] = {0, 0, 0};
-    int rc = 0;
-    for (int t = 0; t < steps && rc == 0; ++t) {
-        for (uint32_t l = 0; l < nlayers && rc == 0; ++l) {
-            LayerHost *L = find_layer(layer0 + l);
-            rc = launch_layer(*L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, g.stream, &ev[6ull * l]);
-        }
-        if (rc) break;
-        if (hipStreamSynchronize(g.stream) != hipSuccess) { rc = -5; break; }
-        for (uint32_t l = 0; l < nlayers; ++l)
-            for (int k = 0; k < 3; ++k) {
-                float ms = 0.0f;
-                if (hipEventElapsedTime(&ms, ev[6ull * l + 2 * k], ev[6ull * l + 2 * k + 1]) != hipSuccess) rc = -5;
-                sum[k] += ms;
-            }
+    std::vector<StepArgs> args;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        const LayerHost &L = *find_layer(layer0 + l);
+        args.push_back(step_args(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr));
     }
-    for (auto &e : ev) (void)hipEventDestroy(e);
-    if (rc) return rc;
-    for (int k = 0; k < 3; ++k) ms_out[k] = (float)(sum[k] / ((double)steps * nlayers));
-    return 0;
+    for (const StepArgs &A : args) {
+        const int rc = launch_step(A, g.stream);
+        if (rc) return rc;
+    }
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    CZ_CHECK(hipEventCreate(&e0), -2);
+    CZ_CHECK(hipEventCreate(&e1), -2);
+    const int kinds[3] = {kRouter, kUp, kDown};
+    int rc = 0;
+    for (int k = 0; k < 3 && rc == 0; ++k) {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        if (hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { rc = -4; break; }
+        for (int r = 0; r < reps && rc == 0; ++r)
+            for (StepArgs A : args) {
+                if (kinds[k] == kDown) A.out = g.work.out;  // leave x untouched
+                rc = launch_step(A, g.stream, kinds[k]);
+                if (rc) break;
+            }
+        const hipError_t ec = hipStreamEndCapture(g.stream, &graph);
+        if (rc == 0 && ec != hipSuccess) rc = -4;
+        if (rc == 0 && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) rc = -4;
+        if (rc == 0 && hipGraphLaunch(exec, g.stream) != hipSuccess) rc = -4;  // warm
+        if (rc == 0 && (hipEventRecord(e0, g.stream) != hipSuccess || hipGraphLaunch(exec, g.stream) != hipSuccess ||
+                        hipEventRecord(e1, g.stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess))
+            rc = -5;
+        float ms = 0.0f;
+        if (rc == 0 && hipEventElapsedTime(&ms, e0, e1) != hipSuccess) rc = -5;
+        if (rc == 0) us_out[k] = (float)(1000.0 * ms / ((double)reps * nlayers));
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc && !g_err[0]) snprintf(g_err, sizeof g_err, "kernel timing pass failed (%d)", rc);
+    return rc;
 }
 
 extern "C" int colizig_hip_expert_slab_read(uint32_t layer, unsigned char *ew, float *es) {

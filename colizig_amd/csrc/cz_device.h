@@ -89,6 +89,12 @@ __device__ inline float cz_dot4_fp8(uint32_t w, float s, const float *x4, float 
 
 // ---------------------------------------------------------------------------
 // wave64 reductions
+// cz_wave_sum / cz_wave_max: xor butterfly through ds_bpermute (any lane
+// order; kept where a specific combine order is part of the contract).
+// cz_wave_sum_dpp / cz_wave_max_dpp: four DPP steps inside each 16-lane row
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+// after which every lane of a row holds the row's result, then the four rows
+// combined as (r0 + r1) + (r2 + r3) from readlane.  The result is uniform.
 // ---------------------------------------------------------------------------
 __device__ inline float cz_wave_sum(float v) {
 #pragma unroll
@@ -100,6 +106,34 @@ __device__ inline float cz_wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, CZ_WAVE));
     return v;
+}
+
+template <int CTRL>
+__device__ inline float cz_dpp(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, 0xF, 0xF, false));
+}
+
+__device__ inline float cz_readlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ inline float cz_wave_sum_dpp(float v) {
+    v = v + cz_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = v + cz_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = v + cz_dpp<0x141>(v);  // row_half_mirror
+    v = v + cz_dpp<0x140>(v);  // row_mirror
+    const float r0 = cz_readlane(v, 0), r1 = cz_readlane(v, 16), r2 = cz_readlane(v, 32), r3 = cz_readlane(v, 48);
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ inline float cz_wave_max_dpp(float v) {
+    v = fmaxf(v, cz_dpp<0xB1>(v));
+    v = fmaxf(v, cz_dpp<0x4E>(v));
+    v = fmaxf(v, cz_dpp<0x141>(v));
+    v = fmaxf(v, cz_dpp<0x140>(v));
+    const float r0 = cz_readlane(v, 0), r1 = cz_readlane(v, 16), r2 = cz_readlane(v, 32), r3 = cz_readlane(v, 48);
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 __device__ inline uint32_t cz_lane() { return threadIdx.x & (CZ_WAVE - 1); }

@@ -9,13 +9,17 @@
 //   shared  gate [SI][H] | up [SI][H] | down [H][SI] E4M3, scales likewise,
 //           sh_gate f32 [H]
 // Decode regime (S tokens, 1..32): three launches per layer
-//   k_router   logits (bit-exact dotF32 order) -> last workgroup of each
-//              token tile: softmax, top-k, gates, shared-expert gate
-//   k_up_*     h[slot][r] = silu(Wg[r].x) * (Wu[r].x) for every (token, slot)
-//              and the shared expert; lanes span the columns of a row,
-//              128-bit loads, dequant in registers, wave reduction
-//   k_down_*   out[t][d] = sum_z (Wd_z[d] . (g_z h_z)) + sgate Wsd[d] . h_sh
-//              (+ residual), the weighted combine fused into the GEMV
+//   k_router_*  logits only, in the reference's dotF32 operation order (one
+//               half-wave per expert row, every row element loaded before the
+//               FMA chains run); optional unit-weight RMSNorm of the input
+//   k_up_*      prologue: one wave turns the token's logits into top-k ids and
+//               gates (softmax, strict '>' scan, f64 gates) in LDS; then
+//               h[slot][r] = silu(Wg[r].x) * (Wu[r].x) for the block's rows,
+//               128-bit loads, E4M3 decoded in registers, wave reduction; the
+//               shared expert's rows and its sigmoid gate ride in the same grid
+//   k_down_*    out[t][d] = xres + sum_z g_z (Wd_z[d] . h_z) + sgate Wsd[d].h_sh,
+//               one wave per output row, all K experts' row loads in flight at
+//               once; the weighted combine is fused into the GEMV in top-k order
 #pragma once
 
 #include "cz_device.h"
@@ -31,6 +35,32 @@ struct LayerDev {
     const uint8_t *sw;     // shared weights (gate|up|down) or null
     const float *ss;       // shared scales (gate|up|down)
     const float *sh_gate;  // [H]
+};
+
+#define CZ_ROUTER_TT 4    // most tokens per router tile
+#define CZ_MAX_E 1024     // experts supported by the top-k wave
+#define CZ_MAX_K 64
+
+// Scratch and routing buffers one layer's three kernels share.
+struct StepArgs {
+    LayerDev L;
+    const float *x;        // [S][H] router input (rms = 0) or raw residual (rms = 1)
+    float *xn;             // [S][H] router input, written by router block 0 when rms = 1
+    float *logits;         // [S][E]
+    uint32_t *idx;         // [S][K] top-k ids in selection order
+    float *gates;          // [S][K]
+    float *sgate;          // [S] shared-expert sigmoid gate
+    float *h;              // [S*K][I] gated products of the routed experts
+    float *hs;             // [S][SI] gated products of the shared expert
+    const float *xres;     // [S][H] residual added to the output (nullable)
+    float *out;            // [S][H]
+    uint32_t *idx_trace;   // nullable [S][K]
+    float *gates_trace;    // nullable [S][K]
+    float *xn_trace;       // nullable [S][H]
+    int S;
+    int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
+    int rms;
+    float eps;
 };
 
 // ---------------------------------------------------------------------------
@@ -93,51 +123,21 @@ __global__ __launch_bounds__(256) void k_gemm_fp8_generic(float *__restrict__ y,
                 acc = __builtin_fmaf(xs[i], v, acc);
             }
         }
-        acc = cz_wave_sum(acc);
+        acc = cz_wave_sum_dpp(acc);
         if (lane == 0) y[(uint64_t)s * O + o] = acc;
     }
 }
 
 // ---------------------------------------------------------------------------
-// router: logits with the reference's dotF32 operation order, then softmax,
-// top-k and gates in the last workgroup of each token tile.
+// router logits in the reference's dotF32 order (matmul.zig:60-82): four
+// accumulators x 8 lanes.  Half-wave lane j (0..31) owns chain j: it
+// accumulates elements i + j of every 32-element step (matmul.zig:65-71),
+// lanes 0..7 then take the 8-element steps (matmul.zig:72-76);
+// total_l = ((0 + acc0_l) + acc1_l) + acc2_l) + acc3_l (matmul.zig:77-78),
+// sum = sequential over l from -0 (matmul.zig:79), scalar fma tail
+// (matmul.zig:80).
 // ---------------------------------------------------------------------------
-#define CZ_ROUTER_TT 4    // most tokens per router tile
-#define CZ_MAX_E 1024     // experts supported by the top-k wave
-#define CZ_MAX_K 64
-
-struct RouterArgs {
-    LayerDev L;
-    const float *x;        // [S][H] raw residual (rms != 0) or router input
-    float *xn;             // [S][H] router input written by tile column 0 (rms != 0)
-    float *logits;         // [S][E]
-    uint32_t *idx;         // [S][K]
-    float *gates;          // [S][K]
-    float *sgate;          // [S] shared-expert sigmoid gate
-    uint32_t *counters;    // [ceil(S/TT)] zero on entry, zero on exit
-    uint32_t *idx_trace;   // nullable [S][K]
-    float *gates_trace;    // nullable [S][K]
-    float *xn_trace;       // nullable [S][H]
-    int S;
-    int tt;                // tokens per tile (1..CZ_ROUTER_TT), tt*H floats of LDS
-    int rms;
-    float eps;
-};
-
-// One logit: 32 lanes (a half wave) hold the reference's 4 accumulators x 8
-// lanes; lane j accumulates elements i + j of every 32-element step
-// (matmul.zig:65-71), lanes 0..7 then take the 8-element steps
-// (matmul.zig:72-76); total_l = ((0 + acc0_l) + acc1_l) + acc2_l) + acc3_l
-// (matmul.zig:77-78), sum = sequential over l (matmul.zig:79), scalar fma
-// tail (matmul.zig:80).  Returns the logit in every lane of the half.
-__device__ inline float cz_router_dot(const float *__restrict__ a, const float *__restrict__ b, uint32_t n,
-                                      uint32_t j, uint32_t half_base) {
-    float acc = 0.0f;
-    uint32_t i = 0;
-    for (; i + 32 <= n; i += 32) acc = __builtin_fmaf(a[i + j], b[i + j], acc);
-    for (; i + 8 <= n; i += 8)
-        if (j < 8) acc = __builtin_fmaf(a[i + j], b[i + j], acc);
-    // total_l for l = j % 8 gathered by lanes j < 8
+__device__ inline float cz_router_combine(float acc, uint32_t j, uint32_t half_base) {
     const float a1 = __shfl(acc, half_base + (j & 7) + 8, CZ_WAVE);
     const float a2 = __shfl(acc, half_base + (j & 7) + 16, CZ_WAVE);
     const float a3 = __shfl(acc, half_base + (j & 7) + 24, CZ_WAVE);
@@ -149,160 +149,297 @@ __device__ inline float cz_router_dot(const float *__restrict__ a, const float *
     float sum = -0.0f;
 #pragma unroll
     for (uint32_t l = 0; l < 8; ++l) sum = sum + __shfl(total, half_base + l, CZ_WAVE);
+    return sum;
+}
+
+// any n: the same order with loads inside the loop
+__device__ inline float cz_router_dot(const float *__restrict__ a, const float *__restrict__ b, uint32_t n,
+                                      uint32_t j, uint32_t half_base) {
+    float acc = 0.0f;
+    uint32_t i = 0;
+    for (; i + 32 <= n; i += 32) acc = __builtin_fmaf(a[i + j], b[i + j], acc);
+    for (; i + 8 <= n; i += 8)
+        if (j < 8) acc = __builtin_fmaf(a[i + j], b[i + j], acc);
+    float sum = cz_router_combine(acc, j, half_base);
     for (; i < n; ++i) sum = __builtin_fmaf(a[i], b[i], sum);
     return sum;
 }
 
-__global__ __launch_bounds__(256) void k_router(RouterArgs A) {
-    const LayerDev &L = A.L;
-    const uint32_t H = L.H, E = L.E, K = L.K;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tile = blockIdx.y;
-    const uint32_t t0 = tile * (uint32_t)A.tt;
-    const uint32_t nt = min((uint32_t)A.tt, (uint32_t)A.S - t0);
-    extern __shared__ float smem[];  // [nt][H] router inputs, then scratch
-    __shared__ float red[4][CZ_ROUTER_TT];
-    __shared__ uint32_t is_last;
-
-    // 1. router input tile into LDS (optionally RMS-normalised)
+// Router input tile of one block into LDS: tokens t0..t0+nt-1, optionally
+// RMS-normalised (x / sqrt(mean(x^2) + eps)); block 0 of the grid publishes
+// the normalised rows.  blockDim.x == 64 (one wave).
+__device__ inline void cz_router_stage_x(const StepArgs &A, float *smem, uint32_t t0, uint32_t nt) {
+    const uint32_t H = A.L.H;
     for (uint32_t t = 0; t < nt; ++t) {
         const float *xs = A.x + (uint64_t)(t0 + t) * H;
         float inv = 1.0f;
         if (A.rms) {
             float ss = 0.0f;
-            for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
+            for (uint32_t i = threadIdx.x; i < H; i += 64) {
                 const float v = xs[i];
                 const float sq = v * v;
                 ss = ss + sq;
             }
-            ss = cz_wave_sum(ss);
-            if (lane == 0) red[wave][t] = ss;
-            __syncthreads();
-            const float tot = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-            inv = 1.0f / sqrtf(tot / (float)H + A.eps);
+            ss = cz_wave_sum_dpp(ss);
+            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
         }
-        for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) {
+        const bool pub = A.rms && blockIdx.x == 0;
+        for (uint32_t i = threadIdx.x; i < H; i += 64) {
             const float v = A.rms ? xs[i] * inv : xs[i];
             smem[t * H + i] = v;
-            if (A.rms && blockIdx.x == 0) {
+            if (pub) {
                 A.xn[(uint64_t)(t0 + t) * H + i] = v;
                 if (A.xn_trace) A.xn_trace[(uint64_t)(t0 + t) * H + i] = v;
             }
         }
     }
-    __syncthreads();
+}
 
-    // 2. logits: half wave per expert row
+// Fast-path staging: NX = H/64 input values per lane, all loaded before the
+// sum of squares is formed, so the RMS costs one L2 round trip per token.
+template <int NX>
+__device__ inline void cz_router_stage_x_reg(const StepArgs &A, float *smem, uint32_t t0, uint32_t nt) {
+    constexpr uint32_t H = 64 * NX;
+    const uint32_t lane = threadIdx.x;
+    const bool pub = A.rms && blockIdx.x == 0;
+    for (uint32_t t = 0; t < nt; ++t) {
+        const float *xs = A.x + (uint64_t)(t0 + t) * H + lane;
+        float xv[NX];
+#pragma unroll
+        for (int i = 0; i < NX; ++i) xv[i] = xs[64 * i];
+        float inv = 1.0f;
+        if (A.rms) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NX; ++i) {
+                const float sq = xv[i] * xv[i];
+                ss = ss + sq;
+            }
+            ss = cz_wave_sum_dpp(ss);
+            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        }
+        float *xo = A.xn + (uint64_t)(t0 + t) * H + lane;
+        float *xt = A.xn_trace ? A.xn_trace + (uint64_t)(t0 + t) * H + lane : nullptr;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const float v = A.rms ? xv[i] * inv : xv[i];
+            smem[t * H + lane + 64 * i] = v;
+            if (pub) {
+                xo[64 * i] = v;
+                if (xt) xt[64 * i] = v;
+            }
+        }
+    }
+}
+
+// One wave per block, two experts per wave (one per half).  NS = H/32: every
+// router element the lane needs is loaded into registers before the input
+// tile is staged and the chains run.
+template <int NS>
+__global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
+    constexpr uint32_t H = 32 * NS;
+    const uint32_t E = A.L.E;
+    const uint32_t lane = threadIdx.x & 63;
     const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
-    const uint32_t e = blockIdx.x * 8 + wave * 2 + half;
-    if (e < E) {
-        const float *wr = L.router + (uint64_t)e * H;
-        for (uint32_t t = 0; t < nt; ++t) {
-            const float lg = cz_router_dot(smem + t * H, wr, H, j, hb);
-            if (j == 0) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
-        }
-    } else {
-        // keep the shuffles of the other half well defined: nothing to do
+    const uint32_t e = blockIdx.x * 2 + half;
+    const uint32_t ec = min(e, E - 1);
+    const uint32_t t0 = blockIdx.y * (uint32_t)A.tt;
+    const uint32_t nt = min((uint32_t)A.tt, (uint32_t)A.S - t0);
+    extern __shared__ float smem[];  // [nt][H]
+    const float *wr = A.L.router + (uint64_t)ec * H + j;
+    float w[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) w[i] = wr[32 * i];
+    cz_router_stage_x_reg<NS / 2>(A, smem, t0, nt);
+    __syncthreads();
+    for (uint32_t t = 0; t < nt; ++t) {
+        const float *xs = smem + t * H + j;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i) acc = __builtin_fmaf(xs[32 * i], w[i], acc);
+        const float lg = cz_router_combine(acc, j, hb);
+        if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
     }
+}
 
-    // 3. last workgroup of this token tile does the routing
-    __threadfence();
+__global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
+    const uint32_t H = A.L.H, E = A.L.E;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
+    const uint32_t e = blockIdx.x * 2 + half;
+    const uint32_t ec = min(e, E - 1);
+    const uint32_t t0 = blockIdx.y * (uint32_t)A.tt;
+    const uint32_t nt = min((uint32_t)A.tt, (uint32_t)A.S - t0);
+    extern __shared__ float smem[];
+    cz_router_stage_x(A, smem, t0, nt);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&A.counters[tile], 1u);
-        is_last = (prev == gridDim.x - 1) ? 1u : 0u;
+    const float *wr = A.L.router + (uint64_t)ec * H;
+    for (uint32_t t = 0; t < nt; ++t) {
+        const float lg = cz_router_dot(smem + t * H, wr, H, j, hb);
+        if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
     }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-
-    // one wave per token of the tile; wave-uniform predicates only, block
-    // barriers outside them
-    constexpr int MAXM = CZ_MAX_E / 64;
-    __shared__ uint32_t s_picks[4][CZ_MAX_K];
-    const bool active = wave < nt;
-    const uint32_t t = t0 + wave;
-    float *vs = smem + (uint64_t)wave * CZ_MAX_E;  // the input tile is no longer needed
-    float v[MAXM];
-    if (active) {
-        const float *lg = A.logits + (uint64_t)t * E;
-        float mx = -INFINITY;
-        bool any = false;
-        // moe.zig:439-440: mx = max over the logits (NaN-ignoring @max)
-#pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            const uint32_t ee = lane + 64 * m;
-            v[m] = ee < E ? lg[ee] : 0.0f;
-            if (ee < E && !(v[m] != v[m])) { mx = any ? fmaxf(mx, v[m]) : v[m]; any = true; }
-        }
-        mx = cz_wave_max(any ? mx : -INFINITY);
-        // moe.zig:441-445: v = exp(l - mx) in f32
-#pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            const uint32_t ee = lane + 64 * m;
-            if (ee < E) {
-                v[m] = cz_expf(v[m] - mx);
-                vs[ee] = v[m];
-            }
-        }
-    }
-    __syncthreads();
-    if (active) {
-        // all = sum_e f64(v_e) in expert order (only used without norm_topk)
-        double all = 0.0;
-        if (!L.norm_topk && lane == 0)
-            for (uint32_t ee = 0; ee < E; ++ee) all += (double)vs[ee];
-        // moe.zig:447-460: K passes of strict '>' argmax over the unchosen,
-        // ties to the lowest expert id; none left -> expert 0
-        uint32_t chosen = 0;  // bit m: expert lane + 64m already picked
-        double top = 0.0;
-        for (uint32_t z = 0; z < K; ++z) {
-            float bv = -1.0f;
-            uint32_t bi = 0xffffffffu;
-#pragma unroll
-            for (int m = 0; m < MAXM; ++m) {
-                const uint32_t ee = lane + 64 * m;
-                if (ee < E && !((chosen >> m) & 1u) && v[m] > bv) { bv = v[m]; bi = ee; }
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, CZ_WAVE);
-                const uint32_t oi = __shfl_xor(bi, off, CZ_WAVE);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-            const uint32_t best = (bi == 0xffffffffu) ? 0u : bi;
-            if ((best & 63u) == lane) chosen |= 1u << (best >> 6);
-            if (lane == 0) s_picks[wave][z] = best;
-            top += (double)vs[best];  // moe.zig:459 in pick order
-        }
-        if (lane == 0) {
-            const double den = L.norm_topk ? top : all;  // moe.zig:461-462
-            for (uint32_t z = 0; z < K; ++z) {
-                const uint32_t b = s_picks[wave][z];
-                const float g = (float)((double)vs[b] / den);
-                A.idx[(uint64_t)t * K + z] = b;
-                A.gates[(uint64_t)t * K + z] = g;
-                if (A.idx_trace) A.idx_trace[(uint64_t)t * K + z] = b;
-                if (A.gates_trace) A.gates_trace[(uint64_t)t * K + z] = g;
-            }
-        }
-        // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
-        if (L.SI != 0) {
-            const float *xs = A.rms ? A.xn + (uint64_t)t * H : A.x + (uint64_t)t * H;
-            float d = 0.0f;
-            for (uint32_t i = lane; i < H; i += 64) {
-                const float prod = xs[i] * L.sh_gate[i];
-                d = d + prod;
-            }
-            d = cz_wave_sum(d);
-            if (lane == 0) A.sgate[t] = cz_sigmoid(d);
-        }
-    }
-    if (threadIdx.x == 0) A.counters[tile] = 0u;
 }
 
 // ---------------------------------------------------------------------------
-// fast-path helpers: NB bytes per lane per row (row width = 64*NB)
+// routing of one token by one wave (moe.zig:435-463): mx = max logit; v =
+// exp(l - mx) in f32; K passes of a strict '>' scan over the unchosen from
+// bv = -1 (ties to the lowest id; none left -> expert 0); top = sum of the
+// picked v in f64 in pick order; den = norm_topk ? top : sum_e f64(v_e) in
+// expert order; gate_z = f32(f64(v_z) / den).  Lane l holds experts
+// l + 64m for m < M (M = ceil(E/64)); values move between lanes by DPP,
+// readlane and ballot only.  Lanes z < K write s_idx[z] / s_gate[z] (LDS),
+// which the block reads after a barrier.  Must be called by a whole wave.
+// ---------------------------------------------------------------------------
+template <int M>
+__device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
+                                       uint32_t *s_idx, float *s_gate) {
+    const uint32_t lane = cz_lane();
+    float v[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) v[m] = lg[min(lane + 64 * m, E - 1)];  // clamped: in bounds
+    // moe.zig:439-440: mx = max over the logits (NaN-ignoring @max)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+        if (lane + 64 * m < E) mx = fmaxf(mx, v[m]);
+    mx = cz_wave_max_dpp(mx);
+    // moe.zig:441-445: v = exp(l - mx) in f32; lanes past E hold NaN, which
+    // never wins a strict '>' comparison or an equality test
+#pragma unroll
+    for (int m = 0; m < M; ++m) v[m] = lane + 64 * m < E ? cz_expf(v[m] - mx) : __builtin_nanf("");
+    double all = 0.0;
+    if (!norm_topk) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            for (uint32_t l = 0; l < 64; ++l)
+                if (64 * m + l < E) all += (double)cz_readlane(v[m], l);
+    }
+    const float v0 = cz_readlane(v[0], 0);
+    uint32_t chosen = 0;  // bit m: expert lane + 64m already picked
+    double top = 0.0;
+    float my_v = 0.0f;    // lane z: value of pick z
+    uint32_t my_i = 0;    // lane z: id of pick z
+    for (uint32_t z = 0; z < K; ++z) {
+        // moe.zig:447-460: the winner is the largest value, lowest id among
+        // equals: the wave max of each lane's best unchosen value, then the
+        // first 64-expert group whose ballot of (v == max) is non-empty,
+        // lowest lane in it (ids of group m all precede those of group m+1).
+        float lb = -1.0f;
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (!((chosen >> m) & 1u) && v[m] > lb) lb = v[m];
+        const float bv = cz_wave_max_dpp(lb);
+        uint32_t best = 0xffffffffu;
+        if (bv > -1.0f) {
+#pragma unroll
+            for (int m = M - 1; m >= 0; --m) {
+                const uint64_t hit = __ballot(!((chosen >> m) & 1u) && v[m] == bv);
+                if (hit) best = 64u * m + (uint32_t)__builtin_ctzll(hit);
+            }
+        }
+        const bool none = best == 0xffffffffu;  // none left -> expert 0
+        if (none) best = 0;
+        const float vb = none ? v0 : bv;        // v[best]
+        if ((best & 63u) == lane) chosen |= 1u << (best >> 6);
+        top += (double)vb;  // moe.zig:459 in pick order
+        if (lane == z) {
+            my_v = vb;
+            my_i = best;
+        }
+    }
+    if (lane < K) {
+        const double den = norm_topk ? top : all;  // moe.zig:461-462
+        s_idx[lane] = my_i;
+        s_gate[lane] = (float)((double)my_v / den);
+    }
+}
+
+__device__ inline void cz_route_wave(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
+                                     uint32_t *s_idx, float *s_gate) {
+    if (E <= 64) cz_route_wave_m<1>(lg, E, K, norm_topk, s_idx, s_gate);
+    else if (E <= 128) cz_route_wave_m<2>(lg, E, K, norm_topk, s_idx, s_gate);
+    else if (E <= 256) cz_route_wave_m<4>(lg, E, K, norm_topk, s_idx, s_gate);
+    else if (E <= 512) cz_route_wave_m<8>(lg, E, K, norm_topk, s_idx, s_gate);
+    else cz_route_wave_m<16>(lg, E, K, norm_topk, s_idx, s_gate);
+}
+
+// Work item of a gate/up block: a routed slot or a shared-expert token.
+struct UpItem {
+    const uint8_t *Wg, *Wu;
+    const float *Sg, *Su;
+    float *out;
+    uint32_t rows, tok, tile;
+    bool routed;
+};
+
+// Resolves block `blk` of a gate/up grid (rows_wg rows per block): routed
+// blocks [0, S*K*tiles_r) run the routing prologue (wave 0) and publish the
+// token's routing from the slot-0 tile-0 block; shared-expert blocks follow,
+// and their tile-0 block computes the token's sigmoid gate.
+__device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const float *xn) {
+    const LayerDev &L = A.L;
+    __shared__ uint32_t s_idx[CZ_MAX_K];
+    __shared__ float s_gate[CZ_MAX_K];
+    const uint32_t wave = threadIdx.x >> 6, lane = cz_lane();
+    const uint32_t tiles_r = (L.I + rows_wg - 1) / rows_wg;
+    const uint32_t nslots = (uint32_t)A.S * L.K;
+    uint32_t blk = blockIdx.x;
+    UpItem it;
+    if (blk < nslots * tiles_r) {
+        const uint32_t slot = blk / tiles_r;
+        it.tile = blk - slot * tiles_r;
+        it.tok = slot / L.K;
+        const uint32_t z = slot - it.tok * L.K;
+        if (wave == 0) cz_route_wave(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate);
+        __syncthreads();
+        if (z == 0 && it.tile == 0 && wave == 0) {
+            for (uint32_t k = lane; k < L.K; k += 64) {
+                const uint64_t o = (uint64_t)it.tok * L.K + k;
+                A.idx[o] = s_idx[k];
+                A.gates[o] = s_gate[k];
+                if (A.idx_trace) A.idx_trace[o] = s_idx[k];
+                if (A.gates_trace) A.gates_trace[o] = s_gate[k];
+            }
+        }
+        const uint32_t e = s_idx[z];
+        const uint8_t *base = L.ew + (uint64_t)e * L.ew_stride;
+        it.Wg = base;
+        it.Wu = base + (uint64_t)L.I * L.H;
+        const float *sb = L.es + (uint64_t)e * L.es_stride;
+        it.Sg = sb;
+        it.Su = sb + (uint64_t)L.nbI * L.nbH;
+        it.out = A.h + (uint64_t)slot * L.I;
+        it.rows = L.I;
+        it.routed = true;
+    } else {
+        blk -= nslots * tiles_r;
+        const uint32_t tiles_s = (L.SI + rows_wg - 1) / rows_wg;
+        it.tok = blk / tiles_s;
+        it.tile = blk - it.tok * tiles_s;
+        it.Wg = L.sw;
+        it.Wu = L.sw + (uint64_t)L.SI * L.H;
+        it.Sg = L.ss;
+        it.Su = L.ss + (uint64_t)L.nbSI * L.nbH;
+        it.out = A.hs + (uint64_t)it.tok * L.SI;
+        it.rows = L.SI;
+        it.routed = false;
+        // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
+        if (it.tile == 0 && wave == 0) {
+            const float *xs = xn + (uint64_t)it.tok * L.H;
+            float d = 0.0f;
+            for (uint32_t i = lane; i < L.H; i += 64) {
+                const float prod = xs[i] * L.sh_gate[i];
+                d = d + prod;
+            }
+            d = cz_wave_sum_dpp(d);
+            if (lane == 0) A.sgate[it.tok] = cz_sigmoid(d);
+        }
+    }
+    return it;
+}
+
+// ---------------------------------------------------------------------------
+// fast-path helpers: NB bytes per lane per row
 // ---------------------------------------------------------------------------
 template <int NB>
 __device__ inline void cz_load_row(const uint8_t *__restrict__ p, uint32_t (&d)[NB / 4]) {
@@ -316,6 +453,10 @@ __device__ inline void cz_load_row(const uint8_t *__restrict__ p, uint32_t (&d)[
     } else if constexpr (NB == 8) {
         const uint2 v = *(const uint2 *)p;
         d[0] = v.x; d[1] = v.y;
+    } else if constexpr (NB == 12) {
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 v = *(const u32x3 *)p;
+        d[0] = v.x; d[1] = v.y; d[2] = v.z;
     } else {
 #pragma unroll
         for (int q = 0; q < NB / 4; ++q) d[q] = ((const uint32_t *)p)[q];
@@ -324,264 +465,204 @@ __device__ inline void cz_load_row(const uint8_t *__restrict__ p, uint32_t (&d)[
 
 template <int NB>
 __device__ inline void cz_load_x(const float *__restrict__ p, float (&x)[NB]) {
-    if constexpr (NB % 4 == 0) {
+    static_assert(NB % 4 == 0, "NB");
 #pragma unroll
-        for (int q = 0; q < NB / 4; ++q) {
-            const float4 v = ((const float4 *)p)[q];
-            x[4 * q + 0] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
-        }
+    for (int q = 0; q < NB / 4; ++q) {
+        const float4 v = ((const float4 *)p)[q];
+        x[4 * q + 0] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
     }
 }
 
-// sum over this lane's NB columns of x * e4m3(w) * scale, scale per dword
-template <int NB>
-__device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)[NB], const float *__restrict__ srow,
-                                   uint32_t col0, float acc) {
-    if constexpr ((CZ_BLOCK % NB) == 0) {
-        const float s = srow[col0 / CZ_BLOCK];  // all of the lane's columns share one block
-#pragma unroll
-        for (int q = 0; q < NB / 4; ++q) acc = cz_dot4_fp8(d[q], s, &x[4 * q], acc);
-    } else {
-#pragma unroll
-        for (int q = 0; q < NB / 4; ++q) acc = cz_dot4_fp8(d[q], srow[(col0 + 4 * q) / CZ_BLOCK], &x[4 * q], acc);
-    }
+// x[0..3] . e4m3(bytes of w), element order = byte order
+__device__ inline float cz_dot4_raw(uint32_t w, const float *x4, float acc) {
+    const cz_float2 lo = cz_fp8x2_lo(w);
+    const cz_float2 hi = cz_fp8x2_hi(w);
+    acc = __builtin_fmaf(x4[0], lo.x, acc);
+    acc = __builtin_fmaf(x4[1], lo.y, acc);
+    acc = __builtin_fmaf(x4[2], hi.x, acc);
+    acc = __builtin_fmaf(x4[3], hi.y, acc);
     return acc;
 }
 
-// ---------------------------------------------------------------------------
-// gate/up + SiLU, fast path: row width H = 64*NB, RW row pairs per wave.
-// Work items: [S*K slots x tiles of I rows] then [S tokens x tiles of SI rows]
-// ---------------------------------------------------------------------------
-template <int NB, int RW>
-__global__ __launch_bounds__(256) void k_up_fast(LayerDev L, const float *__restrict__ xn,
-                                                 const uint32_t *__restrict__ idx, float *__restrict__ h,
-                                                 float *__restrict__ hs, int S) {
-    constexpr int ND = NB / 4;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t rows_wg = 4 * RW;
-    const uint32_t tiles_r = (L.I + rows_wg - 1) / rows_wg;
-    const uint32_t nslots = (uint32_t)S * L.K;
-    uint32_t blk = blockIdx.x;
-    const uint8_t *Wg, *Wu;
-    const float *Sg, *Su;
-    float *out;
-    uint32_t rows, tok, tile, nbr;
-    if (blk < nslots * tiles_r) {
-        const uint32_t slot = blk / tiles_r;
-        tile = blk - slot * tiles_r;
-        tok = slot / L.K;
-        const uint32_t e = idx[slot];
-        const uint8_t *base = L.ew + (uint64_t)e * L.ew_stride;
-        Wg = base;
-        Wu = base + (uint64_t)L.I * L.H;
-        const float *sb = L.es + (uint64_t)e * L.es_stride;
-        Sg = sb;
-        Su = sb + (uint64_t)L.nbI * L.nbH;
-        out = h + (uint64_t)slot * L.I;
-        rows = L.I;
-        nbr = L.nbI;
+// sum over this lane's NB columns [col0, col0+NB) of x * e4m3(w) * scale:
+// the E4M3 products are summed per 128-column block and the block's scale is
+// applied once to that partial sum.
+template <int NB>
+__device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)[NB], const float *__restrict__ srow,
+                                   uint32_t col0) {
+    if constexpr ((CZ_BLOCK % NB) == 0) {
+        // all of the lane's columns share one block
+        float p = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NB / 4; ++q) p = cz_dot4_raw(d[q], &x[4 * q], p);
+        return p * srow[col0 / CZ_BLOCK];
     } else {
-        blk -= nslots * tiles_r;
-        const uint32_t tiles_s = (L.SI + rows_wg - 1) / rows_wg;
-        tok = blk / tiles_s;
-        tile = blk - tok * tiles_s;
-        Wg = L.sw;
-        Wu = L.sw + (uint64_t)L.SI * L.H;
-        Sg = L.ss;
-        Su = L.ss + (uint64_t)L.nbSI * L.nbH;
-        out = hs + (uint64_t)tok * L.SI;
-        rows = L.SI;
-        nbr = L.nbSI;
-    }
-    (void)nbr;
-    const uint32_t r0 = tile * rows_wg + wave * RW;
-    if (r0 >= rows) return;
-    const uint32_t col0 = lane * NB;
-    float xv[NB];
-    cz_load_x<NB>(xn + (uint64_t)tok * L.H + col0, xv);
-    uint32_t dg[RW][ND], du[RW][ND];
+        float acc = 0.0f;
 #pragma unroll
-    for (int rr = 0; rr < RW; ++rr) {
-        const uint32_t rc = min(r0 + rr, rows - 1);
-        cz_load_row<NB>(Wg + (uint64_t)rc * L.H + col0, dg[rr]);
-        cz_load_row<NB>(Wu + (uint64_t)rc * L.H + col0, du[rr]);
-    }
-#pragma unroll
-    for (int rr = 0; rr < RW; ++rr) {
-        const uint32_t r = r0 + rr;
-        const uint32_t rc = min(r, rows - 1);
-        const float *sgr = Sg + (uint64_t)(rc / CZ_BLOCK) * L.nbH;
-        const float *sur = Su + (uint64_t)(rc / CZ_BLOCK) * L.nbH;
-        float ag = cz_row_dot<NB>(dg[rr], xv, sgr, col0, 0.0f);
-        float au = cz_row_dot<NB>(du[rr], xv, sur, col0, 0.0f);
-        ag = cz_wave_sum(ag);
-        au = cz_wave_sum(au);
-        if (lane == (uint32_t)rr && r < rows) out[r] = cz_silu(ag) * au;
+        for (int q = 0; q < NB / 4; ++q) {
+            const float p = cz_dot4_raw(d[q], &x[4 * q], 0.0f);
+            acc = __builtin_fmaf(p, srow[(col0 + 4 * q) / CZ_BLOCK], acc);
+        }
+        return acc;
     }
 }
 
 // ---------------------------------------------------------------------------
-// down + weighted combine (+ shared expert, + residual), fast path:
-// routed row width I = 64*NBI, shared row width SI = 64*NBS (NBS 0 = none).
+// gate/up + SiLU, fast path: row width H = 64*NB, RW rows per wave, both
+// matrices' rows loaded before any is reduced.
 // ---------------------------------------------------------------------------
-template <int NBI, int NBS, int RD>
-__global__ __launch_bounds__(256) void k_down_fast(LayerDev L, const float *__restrict__ h,
-                                                   const float *__restrict__ hs, const uint32_t *__restrict__ idx,
-                                                   const float *__restrict__ gates, const float *__restrict__ sgate,
-                                                   const float *xres, float *out, int S) {
-    constexpr int NDI = NBI / 4;
+template <int NB, int RW>
+__global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
+    constexpr int ND = NB / 4;
+    const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t rows_wg = 4 * RD;
-    const uint32_t tiles_h = (L.H + rows_wg - 1) / rows_wg;
+    const float *xn = A.rms ? A.xn : A.x;
+    const UpItem it = cz_up_item(A, 4 * RW, xn);
+    const uint32_t r0 = it.tile * 4 * RW + wave * RW;
+    if (r0 >= it.rows) return;
+    const uint32_t col0 = lane * NB;
+    uint32_t dg[RW][ND], du[RW][ND];
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+        const uint32_t rc = min(r0 + rr, it.rows - 1);
+        cz_load_row<NB>(it.Wg + (uint64_t)rc * L.H + col0, dg[rr]);
+        cz_load_row<NB>(it.Wu + (uint64_t)rc * L.H + col0, du[rr]);
+    }
+    float xv[NB];
+    cz_load_x<NB>(xn + (uint64_t)it.tok * L.H + col0, xv);
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any is consumed
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+        const uint32_t r = r0 + rr;
+        const uint32_t rc = min(r, it.rows - 1);
+        float ag = cz_row_dot<NB>(dg[rr], xv, it.Sg + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0);
+        float au = cz_row_dot<NB>(du[rr], xv, it.Su + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0);
+        ag = cz_wave_sum_dpp(ag);
+        au = cz_wave_sum_dpp(au);
+        if (lane == (uint32_t)rr && r < it.rows) it.out[r] = cz_silu(ag) * au;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// down + weighted combine (+ shared expert, + residual), fast path: one wave
+// per output row; routed row width I = 64*NBI, shared row width SI = 64*NBS
+// (NBS 0 = none).  Experts are taken KC at a time, every load of a chunk
+// issued before its arithmetic.
+// ---------------------------------------------------------------------------
+template <int NBI, int NBS, int KC>
+__global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
+    constexpr int NDI = NBI / 4;
+    const LayerDev &L = A.L;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tiles_h = (L.H + 3) / 4;
     const uint32_t tok = blockIdx.x / tiles_h, tile = blockIdx.x - tok * tiles_h;
-    const uint32_t r0 = tile * rows_wg + wave * RD;
-    if (r0 >= L.H || tok >= (uint32_t)S) return;
-    float acc[RD];
-#pragma unroll
-    for (int rr = 0; rr < RD; ++rr) acc[rr] = 0.0f;
+    const uint32_t r = tile * 4 + wave;
+    if (r >= L.H || tok >= (uint32_t)A.S) return;
     const uint32_t col0 = lane * NBI;
-    for (uint32_t z = 0; z < L.K; ++z) {
-        const uint32_t slot = tok * L.K + z;
-        const uint32_t e = idx[slot];
-        const float g = gates[slot];
-        float hv[NBI];
-        cz_load_x<NBI>(h + (uint64_t)slot * L.I + col0, hv);
+    // the token's K expert ids and gates, one per lane, broadcast by readlane
+    const uint32_t my_e = lane < L.K ? A.idx[(uint64_t)tok * L.K + lane] : 0u;
+    const float my_g = lane < L.K ? A.gates[(uint64_t)tok * L.K + lane] : 0.0f;
+    float acc = 0.0f;
+    for (uint32_t z0 = 0; z0 < L.K; z0 += KC) {
+        uint32_t dd[KC][NDI];
+        float hv[KC][NBI];
+        const float *srow[KC];
 #pragma unroll
-        for (int c = 0; c < NBI; ++c) hv[c] = hv[c] * g;
-        const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
-        const float *Sd = L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH;
-        uint32_t dd[RD][NDI];
-#pragma unroll
-        for (int rr = 0; rr < RD; ++rr) {
-            const uint32_t rc = min(r0 + rr, L.H - 1);
-            cz_load_row<NBI>(Wd + (uint64_t)rc * L.I + col0, dd[rr]);
+        for (int c = 0; c < KC; ++c) {
+            const uint32_t z = min(z0 + c, L.K - 1);
+            const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_e, z), L.E - 1);
+            const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
+            srow[c] = L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI;
+            cz_load_row<NBI>(Wd + (uint64_t)r * L.I + col0, dd[c]);
         }
 #pragma unroll
-        for (int rr = 0; rr < RD; ++rr) {
-            const uint32_t rc = min(r0 + rr, L.H - 1);
-            acc[rr] = cz_row_dot<NBI>(dd[rr], hv, Sd + (uint64_t)(rc / CZ_BLOCK) * L.nbI, col0, acc[rr]);
+        for (int c = 0; c < KC; ++c) {
+            const uint32_t z = min(z0 + c, L.K - 1);
+            cz_load_x<NBI>(A.h + (uint64_t)(tok * L.K + z) * L.I + col0, hv[c]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the chunk's loads are all in flight
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const uint32_t z = min(z0 + c, L.K - 1);
+            const float g = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_g), z));
+            const float p = cz_row_dot<NBI>(dd[c], hv[c], srow[c], col0);
+            if (z0 + c < L.K) acc = __builtin_fmaf(g, p, acc);
         }
     }
     if constexpr (NBS > 0) {
         constexpr int NDS = NBS / 4;
         const uint32_t cs0 = lane * NBS;
+        uint32_t dd[NDS];
+        cz_load_row<NBS>(L.sw + 2ull * L.SI * L.H + (uint64_t)r * L.SI + cs0, dd);
         float hv[NBS];
-        cz_load_x<NBS>(hs + (uint64_t)tok * L.SI + cs0, hv);
-        const float sgv = sgate[tok];
-#pragma unroll
-        for (int c = 0; c < NBS; ++c) hv[c] = hv[c] * sgv;
-        const uint8_t *Wd = L.sw + 2ull * L.SI * L.H;
-        const float *Sd = L.ss + 2ull * L.nbSI * L.nbH;
-#pragma unroll
-        for (int rr = 0; rr < RD; ++rr) {
-            const uint32_t rc = min(r0 + rr, L.H - 1);
-            uint32_t dd[NDS];
-            cz_load_row<NBS>(Wd + (uint64_t)rc * L.SI + cs0, dd);
-            acc[rr] = cz_row_dot<NBS>(dd, hv, Sd + (uint64_t)(rc / CZ_BLOCK) * L.nbSI, cs0, acc[rr]);
-        }
+        cz_load_x<NBS>(A.hs + (uint64_t)tok * L.SI + cs0, hv);
+        const float p = cz_row_dot<NBS>(dd, hv, L.ss + 2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI, cs0);
+        acc = __builtin_fmaf(A.sgate[tok], p, acc);
     }
-#pragma unroll
-    for (int rr = 0; rr < RD; ++rr) {
-        const float tot = cz_wave_sum(acc[rr]);
-        const uint32_t r = r0 + rr;
-        if (lane == (uint32_t)rr && r < L.H) {
-            const uint64_t o = (uint64_t)tok * L.H + r;
-            out[o] = (xres ? xres[o] : 0.0f) + tot;
-        }
+    const float tot = cz_wave_sum_dpp(acc);
+    if (lane == 0) {
+        const uint64_t o = (uint64_t)tok * L.H + r;
+        A.out[o] = (A.xres ? A.xres[o] : 0.0f) + tot;
     }
 }
 
 // ---------------------------------------------------------------------------
-// generic (any H, I, SI) forms of the two expert kernels: one wave per row
-// (pair), lanes stride single columns.  Used for shapes the fast paths do
-// not cover (widths that are not 64 * {4,8,12,16,24,32,48,64}).
+// generic (any H, I, SI) forms of the two expert kernels: one wave per row,
+// lanes stride single columns.  Used for shapes the fast paths do not cover.
 // ---------------------------------------------------------------------------
 __device__ inline float cz_dot_fp8_strided(const uint8_t *__restrict__ w, const float *__restrict__ srow,
-                                           const float *__restrict__ x, uint32_t n, uint32_t lane, float scale_x) {
+                                           const float *__restrict__ x, uint32_t n, uint32_t lane) {
     float acc = 0.0f;
     for (uint32_t i = lane; i < n; i += 64) {
         const float v = __builtin_amdgcn_cvt_f32_fp8((int)w[i], 0) * srow[i / CZ_BLOCK];
-        const float xi = x[i] * scale_x;
-        acc = __builtin_fmaf(xi, v, acc);
+        acc = __builtin_fmaf(x[i], v, acc);
     }
     return acc;
 }
 
-__global__ __launch_bounds__(256) void k_up_generic(LayerDev L, const float *__restrict__ xn,
-                                                    const uint32_t *__restrict__ idx, float *__restrict__ h,
-                                                    float *__restrict__ hs, int S) {
+__global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
+    const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tiles_r = (L.I + 3) / 4;
-    const uint32_t nslots = (uint32_t)S * L.K;
-    uint32_t blk = blockIdx.x;
-    const uint8_t *Wg, *Wu;
-    const float *Sg, *Su;
-    float *out;
-    uint32_t rows, tok, tile;
-    if (blk < nslots * tiles_r) {
-        const uint32_t slot = blk / tiles_r;
-        tile = blk - slot * tiles_r;
-        tok = slot / L.K;
-        const uint32_t e = idx[slot];
-        const uint8_t *base = L.ew + (uint64_t)e * L.ew_stride;
-        Wg = base;
-        Wu = base + (uint64_t)L.I * L.H;
-        const float *sb = L.es + (uint64_t)e * L.es_stride;
-        Sg = sb;
-        Su = sb + (uint64_t)L.nbI * L.nbH;
-        out = h + (uint64_t)slot * L.I;
-        rows = L.I;
-    } else {
-        blk -= nslots * tiles_r;
-        const uint32_t tiles_s = (L.SI + 3) / 4;
-        tok = blk / tiles_s;
-        tile = blk - tok * tiles_s;
-        Wg = L.sw;
-        Wu = L.sw + (uint64_t)L.SI * L.H;
-        Sg = L.ss;
-        Su = L.ss + (uint64_t)L.nbSI * L.nbH;
-        out = hs + (uint64_t)tok * L.SI;
-        rows = L.SI;
-    }
-    const uint32_t r = tile * 4 + wave;
-    if (r >= rows) return;
-    const float *xs = xn + (uint64_t)tok * L.H;
-    float ag = cz_dot_fp8_strided(Wg + (uint64_t)r * L.H, Sg + (uint64_t)(r / CZ_BLOCK) * L.nbH, xs, L.H, lane, 1.0f);
-    float au = cz_dot_fp8_strided(Wu + (uint64_t)r * L.H, Su + (uint64_t)(r / CZ_BLOCK) * L.nbH, xs, L.H, lane, 1.0f);
-    ag = cz_wave_sum(ag);
-    au = cz_wave_sum(au);
-    if (lane == 0) out[r] = cz_silu(ag) * au;
+    const float *xn = A.rms ? A.xn : A.x;
+    const UpItem it = cz_up_item(A, 4, xn);
+    const uint32_t r = it.tile * 4 + wave;
+    if (r >= it.rows) return;
+    const float *xs = xn + (uint64_t)it.tok * L.H;
+    float ag = cz_dot_fp8_strided(it.Wg + (uint64_t)r * L.H, it.Sg + (uint64_t)(r / CZ_BLOCK) * L.nbH, xs, L.H, lane);
+    float au = cz_dot_fp8_strided(it.Wu + (uint64_t)r * L.H, it.Su + (uint64_t)(r / CZ_BLOCK) * L.nbH, xs, L.H, lane);
+    ag = cz_wave_sum_dpp(ag);
+    au = cz_wave_sum_dpp(au);
+    if (lane == 0) it.out[r] = cz_silu(ag) * au;
 }
 
-__global__ __launch_bounds__(256) void k_down_generic(LayerDev L, const float *__restrict__ h,
-                                                      const float *__restrict__ hs, const uint32_t *__restrict__ idx,
-                                                      const float *__restrict__ gates,
-                                                      const float *__restrict__ sgate, const float *xres, float *out,
-                                                      int S) {
+__global__ __launch_bounds__(256) void k_down_generic(StepArgs A) {
+    const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tiles_h = (L.H + 3) / 4;
     const uint32_t tok = blockIdx.x / tiles_h, tile = blockIdx.x - tok * tiles_h;
     const uint32_t r = tile * 4 + wave;
-    if (r >= L.H || tok >= (uint32_t)S) return;
+    if (r >= L.H || tok >= (uint32_t)A.S) return;
     float acc = 0.0f;
     for (uint32_t z = 0; z < L.K; ++z) {
         const uint32_t slot = tok * L.K + z;
-        const uint32_t e = idx[slot];
+        const uint32_t e = A.idx[slot];
         const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
         const float *Sd = L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH;
-        acc += cz_dot_fp8_strided(Wd + (uint64_t)r * L.I, Sd + (uint64_t)(r / CZ_BLOCK) * L.nbI,
-                                  h + (uint64_t)slot * L.I, L.I, lane, gates[slot]);
+        const float p = cz_dot_fp8_strided(Wd + (uint64_t)r * L.I, Sd + (uint64_t)(r / CZ_BLOCK) * L.nbI,
+                                           A.h + (uint64_t)slot * L.I, L.I, lane);
+        acc = __builtin_fmaf(A.gates[slot], p, acc);
     }
     if (L.SI != 0) {
         const uint8_t *Wd = L.sw + 2ull * L.SI * L.H;
         const float *Sd = L.ss + 2ull * L.nbSI * L.nbH;
-        acc += cz_dot_fp8_strided(Wd + (uint64_t)r * L.SI, Sd + (uint64_t)(r / CZ_BLOCK) * L.nbSI,
-                                  hs + (uint64_t)tok * L.SI, L.SI, lane, sgate[tok]);
+        const float p = cz_dot_fp8_strided(Wd + (uint64_t)r * L.SI, Sd + (uint64_t)(r / CZ_BLOCK) * L.nbSI,
+                                           A.hs + (uint64_t)tok * L.SI, L.SI, lane);
+        acc = __builtin_fmaf(A.sgate[tok], p, acc);
     }
-    acc = cz_wave_sum(acc);
+    acc = cz_wave_sum_dpp(acc);
     if (lane == 0) {
         const uint64_t o = (uint64_t)tok * L.H + r;
-        out[o] = (xres ? xres[o] : 0.0f) + acc;
+        A.out[o] = (A.xres ? A.xres[o] : 0.0f) + acc;
     }
 }
 

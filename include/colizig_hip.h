@@ -137,12 +137,13 @@ int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlayers, float 
 int colizig_hip_graph_launch(int64_t handle, void *stream);
 void colizig_hip_graph_destroy(int64_t handle);
 
-/* Timing pass: runs the chain eagerly `steps` times with HIP events around
- * each kernel on the library stream; ms_out[3] receives the mean duration
- * (ms) of the router, gate/up and down kernels per layer.  x_dev advances as
- * in colizig_hip_chain_decode. */
-int colizig_hip_chain_profile(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, int steps,
-                              float *ms_out);
+/* Per-kernel timing: one chain step (x_dev advances as in
+ * colizig_hip_chain_decode), then for each of the router, gate/up and down
+ * kernels a HIP graph of `reps` passes over the layers launching only that
+ * kernel is replayed between two events on the library stream.  us_out[3]
+ * receives each kernel's mean duration per launch in microseconds. */
+int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, int reps,
+                                   float *us_out);
 
 /* Fills a registered layer (router, every expert, shared expert) with
  * seeded synthetic weights directly in HBM: router and sh_gate f32
