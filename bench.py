@@ -32,6 +32,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
+# HBM bytes per launch of the gate/up kernel on this workload, measured with
+# rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by what the same
+# counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0):
+# 12422.1 KiB fetched, 24.1 KiB written per dispatch.
+UP_TRAFFIC_BYTES = int(round((12422.1 * 2.0 + 24.1) * 1024))
+
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
 
@@ -67,10 +73,16 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     from colizig_amd import _lib, moe
 
@@ -157,7 +169,8 @@ def main():
         "dtype": "e4m3-weights/f32-accumulate",
         "data": "synthetic (seeded N(0,0.02) weights generated in HBM, N(0,1) hidden state)",
         "config": {**c, "parallelism": "none (1 GPU)", "global_batch": 1, "seq_len": 1},
-        "hbm_gbs_per_token": round(tok_bytes * tok_s / 1e9, 1),
+        "step_hbm_gbs": round(tok_bytes * tok_s / 1e9, 1),
+        "step_hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
             "kernel": "k_up_fast (top-k + gate/up GEMV + SiLU, 8 experts)",
@@ -165,7 +178,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(up_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": UP_TRAFFIC_BYTES,
             "bytes_per_launch": b["up"],
             "avg_launch_us": round(up_us, 3),
         },
@@ -176,6 +189,21 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def calibrate_copy(mib: int) -> None:
+    """A plain copy kernel of known size: under rocprofv3 --pmc its FETCH_SIZE /
+    WRITE_SIZE give the counters' scale (bytes counted per byte moved)."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copied {mib} MiB x 3")
 
 
 def parity_check(hip, moe, layers, xb, c, eps):
@@ -236,7 +264,8 @@ def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
     t0 = time.time()
     hosts = [orc.OracleLayer(host_layer(hip, L, c)) for L in layers]
     copy_s = time.time() - t0
-    threads = len(os.sched_getaffinity(0))
+    # the GPU box's CPU share is 16 cores per GPU, whatever the affinity mask shows
+    threads = min(len(os.sched_getaffinity(0)), 16)
     orc.lib().czo_parallel_enable(threads)
     x = x0.copy()
     n = 0

@@ -217,29 +217,42 @@ void launch_router(const StepArgs &A, hipStream_t st) {
     }
 }
 
-template <int NB>
-void launch_up_t(const StepArgs &A, hipStream_t st) {
+template <int NB, int M>
+void launch_up_nm(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
-    const uint32_t rows_wg = 4 * kUpRows;
-    const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
-                            (L.SI ? (uint32_t)A.S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
-    k_up_fast<NB, kUpRows><<<blocks, 256, 0, st>>>(A);
+    if constexpr (NB == 0) {
+        const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)A.S * ((L.SI + 3) / 4) : 0u);
+        k_up_generic<M><<<blocks, 256, 0, st>>>(A);
+    } else {
+        const uint32_t rows_wg = 4 * kUpRows;
+        const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
+                                (L.SI ? (uint32_t)A.S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
+        k_up_fast<NB, kUpRows, M><<<blocks, 256, 0, st>>>(A);
+    }
 }
 
+template <int NB>
+void launch_up_n(const StepArgs &A, hipStream_t st) {
+    switch (cz_route_groups(A.L.E)) {
+        case 1: launch_up_nm<NB, 1>(A, st); return;
+        case 2: launch_up_nm<NB, 2>(A, st); return;
+        case 4: launch_up_nm<NB, 4>(A, st); return;
+        case 8: launch_up_nm<NB, 8>(A, st); return;
+        default: launch_up_nm<NB, 16>(A, st); return;
+    }
+}
+
+// fast path for H = 64 * {4, 8, 16, 32, 48, 64}, generic kernel otherwise
 void launch_up(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
     switch ((L.H % 64) ? 0u : L.H / 64) {
-        case 4: launch_up_t<4>(A, st); return;
-        case 8: launch_up_t<8>(A, st); return;
-        case 16: launch_up_t<16>(A, st); return;
-        case 32: launch_up_t<32>(A, st); return;
-        case 48: launch_up_t<48>(A, st); return;
-        case 64: launch_up_t<64>(A, st); return;
-        default: {
-            const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)A.S * ((L.SI + 3) / 4) : 0u);
-            k_up_generic<<<blocks, 256, 0, st>>>(A);
-            return;
-        }
+        case 4: launch_up_n<4>(A, st); return;
+        case 8: launch_up_n<8>(A, st); return;
+        case 16: launch_up_n<16>(A, st); return;
+        case 32: launch_up_n<32>(A, st); return;
+        case 48: launch_up_n<48>(A, st); return;
+        case 64: launch_up_n<64>(A, st); return;
+        default: launch_up_n<0>(A, st); return;
     }
 }
 

@@ -354,13 +354,9 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
     }
 }
 
-__device__ inline void cz_route_wave(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
-                                     uint32_t *s_idx, float *s_gate) {
-    if (E <= 64) cz_route_wave_m<1>(lg, E, K, norm_topk, s_idx, s_gate);
-    else if (E <= 128) cz_route_wave_m<2>(lg, E, K, norm_topk, s_idx, s_gate);
-    else if (E <= 256) cz_route_wave_m<4>(lg, E, K, norm_topk, s_idx, s_gate);
-    else if (E <= 512) cz_route_wave_m<8>(lg, E, K, norm_topk, s_idx, s_gate);
-    else cz_route_wave_m<16>(lg, E, K, norm_topk, s_idx, s_gate);
+// expert groups of 64 a routing wave holds for E experts
+__host__ __device__ constexpr int cz_route_groups(uint32_t E) {
+    return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
 }
 
 // Work item of a gate/up block: a routed slot or a shared-expert token.
@@ -376,7 +372,8 @@ struct UpItem {
 // blocks [0, S*K*tiles_r) run the routing prologue (wave 0) and publish the
 // token's routing from the slot-0 tile-0 block; shared-expert blocks follow,
 // and their tile-0 block computes the token's sigmoid gate.
-__device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const float *xn) {
+template <int M>
+__device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const float *xn, float4 *xs_lds = nullptr) {
     const LayerDev &L = A.L;
     __shared__ uint32_t s_idx[CZ_MAX_K];
     __shared__ float s_gate[CZ_MAX_K];
@@ -385,12 +382,21 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
     const uint32_t nslots = (uint32_t)A.S * L.K;
     uint32_t blk = blockIdx.x;
     UpItem it;
+    // the block's token row of the router input, staged in LDS while the
+    // routing runs (H/4 float4, H a multiple of 4)
+    auto stage_x = [&](uint32_t tok) {
+        if (xs_lds) {
+            const float4 *src = (const float4 *)(xn + (uint64_t)tok * L.H);
+            for (uint32_t i = threadIdx.x; i < L.H / 4; i += blockDim.x) xs_lds[i] = src[i];
+        }
+    };
     if (blk < nslots * tiles_r) {
         const uint32_t slot = blk / tiles_r;
         it.tile = blk - slot * tiles_r;
         it.tok = slot / L.K;
         const uint32_t z = slot - it.tok * L.K;
-        if (wave == 0) cz_route_wave(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate);
+        stage_x(it.tok);
+        if (wave == 0) cz_route_wave_m<M>(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate);
         __syncthreads();
         if (z == 0 && it.tile == 0 && wave == 0) {
             for (uint32_t k = lane; k < L.K; k += 64) {
@@ -423,6 +429,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         it.out = A.hs + (uint64_t)it.tok * L.SI;
         it.rows = L.SI;
         it.routed = false;
+        stage_x(it.tok);
         // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         if (it.tile == 0 && wave == 0) {
             const float *xs = xn + (uint64_t)it.tok * L.H;
@@ -434,6 +441,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
             d = cz_wave_sum_dpp(d);
             if (lane == 0) A.sgate[it.tok] = cz_sigmoid(d);
         }
+        __syncthreads();
     }
     return it;
 }
@@ -484,80 +492,99 @@ __device__ inline float cz_dot4_raw(uint32_t w, const float *x4, float acc) {
     return acc;
 }
 
-// sum over this lane's NB columns [col0, col0+NB) of x * e4m3(w) * scale:
-// the E4M3 products are summed per 128-column block and the block's scale is
-// applied once to that partial sum.
+// Scales a lane needs for its NB columns [col0, col0+NB) of one row: one per
+// dword, read from the row's scale row before any weight is consumed.
 template <int NB>
-__device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)[NB], const float *__restrict__ srow,
-                                   uint32_t col0) {
-    if constexpr ((CZ_BLOCK % NB) == 0) {
-        // all of the lane's columns share one block
+struct RowScales {
+    static constexpr int N = (CZ_BLOCK % NB) == 0 ? 1 : NB / 4;
+    float s[N];
+};
+
+template <int NB>
+__device__ inline void cz_load_scales(const float *__restrict__ srow, uint32_t col0, RowScales<NB> &rs) {
+    if constexpr (RowScales<NB>::N == 1) {
+        rs.s[0] = srow[col0 / CZ_BLOCK];  // all of the lane's columns share one block
+    } else {
+#pragma unroll
+        for (int q = 0; q < NB / 4; ++q) rs.s[q] = srow[(col0 + 4 * q) / CZ_BLOCK];
+    }
+}
+
+// sum over the lane's NB columns of x * e4m3(w) * scale: the E4M3 products
+// are summed per 128-column block and the block's scale is applied once to
+// that partial sum.
+template <int NB>
+__device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)[NB], const RowScales<NB> &rs) {
+    if constexpr (RowScales<NB>::N == 1) {
         float p = 0.0f;
 #pragma unroll
         for (int q = 0; q < NB / 4; ++q) p = cz_dot4_raw(d[q], &x[4 * q], p);
-        return p * srow[col0 / CZ_BLOCK];
+        return p * rs.s[0];
     } else {
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < NB / 4; ++q) {
             const float p = cz_dot4_raw(d[q], &x[4 * q], 0.0f);
-            acc = __builtin_fmaf(p, srow[(col0 + 4 * q) / CZ_BLOCK], acc);
+            acc = __builtin_fmaf(p, rs.s[q], acc);
         }
         return acc;
     }
 }
 
 // ---------------------------------------------------------------------------
-// gate/up + SiLU, fast path: row width H = 64*NB, RW rows per wave, both
-// matrices' rows loaded before any is reduced.
+// gate/up + SiLU, fast path: row width H = 64*NB, RW rows per wave; weights,
+// scales and the input slice are all requested before any is consumed.
 // ---------------------------------------------------------------------------
 template <int NB, int RW>
-__global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
+__device__ inline void cz_up_rows(const StepArgs &A, const UpItem &it, const float *xs_lds, uint32_t r0, uint32_t lane) {
     constexpr int ND = NB / 4;
     const LayerDev &L = A.L;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float *xn = A.rms ? A.xn : A.x;
-    const UpItem it = cz_up_item(A, 4 * RW, xn);
-    const uint32_t r0 = it.tile * 4 * RW + wave * RW;
-    if (r0 >= it.rows) return;
     const uint32_t col0 = lane * NB;
     uint32_t dg[RW][ND], du[RW][ND];
+    RowScales<NB> sg[RW], su[RW];
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) {
         const uint32_t rc = min(r0 + rr, it.rows - 1);
         cz_load_row<NB>(it.Wg + (uint64_t)rc * L.H + col0, dg[rr]);
         cz_load_row<NB>(it.Wu + (uint64_t)rc * L.H + col0, du[rr]);
+        cz_load_scales<NB>(it.Sg + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0, sg[rr]);
+        cz_load_scales<NB>(it.Su + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0, su[rr]);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every weight and scale load is in flight
     float xv[NB];
-    cz_load_x<NB>(xn + (uint64_t)it.tok * L.H + col0, xv);
-    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before any is consumed
+    cz_load_x<NB>(xs_lds + col0, xv);
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) {
         const uint32_t r = r0 + rr;
-        const uint32_t rc = min(r, it.rows - 1);
-        float ag = cz_row_dot<NB>(dg[rr], xv, it.Sg + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0);
-        float au = cz_row_dot<NB>(du[rr], xv, it.Su + (uint64_t)(rc / CZ_BLOCK) * L.nbH, col0);
+        float ag = cz_row_dot<NB>(dg[rr], xv, sg[rr]);
+        float au = cz_row_dot<NB>(du[rr], xv, su[rr]);
         ag = cz_wave_sum_dpp(ag);
         au = cz_wave_sum_dpp(au);
         if (lane == (uint32_t)rr && r < it.rows) it.out[r] = cz_silu(ag) * au;
     }
 }
 
+template <int NB, int RW, int M>
+__global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
+    __shared__ float4 xs[NB * 16];  // the token's router input, H = 64*NB floats
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *xn = A.rms ? A.xn : A.x;
+    const UpItem it = cz_up_item<M>(A, 4 * RW, xn, xs);
+    const uint32_t r0 = it.tile * 4 * RW + wave * RW;
+    if (r0 >= it.rows) return;
+    cz_up_rows<NB, RW>(A, it, (const float *)xs, r0, lane);
+}
+
 // ---------------------------------------------------------------------------
 // down + weighted combine (+ shared expert, + residual), fast path: one wave
 // per output row; routed row width I = 64*NBI, shared row width SI = 64*NBS
-// (NBS 0 = none).  Experts are taken KC at a time, every load of a chunk
-// issued before its arithmetic.
+// (NBS 0 = none).  Experts are taken KC at a time, every weight, scale and h
+// load of a chunk issued before its arithmetic.
 // ---------------------------------------------------------------------------
 template <int NBI, int NBS, int KC>
-__global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
+__device__ inline void cz_down_row(const StepArgs &A, uint32_t tok, uint32_t r, uint32_t lane) {
     constexpr int NDI = NBI / 4;
     const LayerDev &L = A.L;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tiles_h = (L.H + 3) / 4;
-    const uint32_t tok = blockIdx.x / tiles_h, tile = blockIdx.x - tok * tiles_h;
-    const uint32_t r = tile * 4 + wave;
-    if (r >= L.H || tok >= (uint32_t)A.S) return;
     const uint32_t col0 = lane * NBI;
     // the token's K expert ids and gates, one per lane, broadcast by readlane
     const uint32_t my_e = lane < L.K ? A.idx[(uint64_t)tok * L.K + lane] : 0u;
@@ -565,15 +592,16 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
     float acc = 0.0f;
     for (uint32_t z0 = 0; z0 < L.K; z0 += KC) {
         uint32_t dd[KC][NDI];
+        RowScales<NBI> sd[KC];
         float hv[KC][NBI];
-        const float *srow[KC];
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
             const uint32_t z = min(z0 + c, L.K - 1);
             const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_e, z), L.E - 1);
             const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
-            srow[c] = L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI;
             cz_load_row<NBI>(Wd + (uint64_t)r * L.I + col0, dd[c]);
+            cz_load_scales<NBI>(L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI,
+                                col0, sd[c]);
         }
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
@@ -584,8 +612,8 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
             const uint32_t z = min(z0 + c, L.K - 1);
-            const float g = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_g), z));
-            const float p = cz_row_dot<NBI>(dd[c], hv[c], srow[c], col0);
+            const float g = cz_readlane(my_g, z);
+            const float p = cz_row_dot<NBI>(dd[c], hv[c], sd[c]);
             if (z0 + c < L.K) acc = __builtin_fmaf(g, p, acc);
         }
     }
@@ -593,17 +621,32 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
         constexpr int NDS = NBS / 4;
         const uint32_t cs0 = lane * NBS;
         uint32_t dd[NDS];
+        RowScales<NBS> ss;
         cz_load_row<NBS>(L.sw + 2ull * L.SI * L.H + (uint64_t)r * L.SI + cs0, dd);
+        cz_load_scales<NBS>(L.ss + 2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI, cs0, ss);
         float hv[NBS];
         cz_load_x<NBS>(A.hs + (uint64_t)tok * L.SI + cs0, hv);
-        const float p = cz_row_dot<NBS>(dd, hv, L.ss + 2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI, cs0);
-        acc = __builtin_fmaf(A.sgate[tok], p, acc);
+        const float sgv = A.sgate[tok];
+        __builtin_amdgcn_sched_barrier(0);
+        const float p = cz_row_dot<NBS>(dd, hv, ss);
+        acc = __builtin_fmaf(sgv, p, acc);
     }
     const float tot = cz_wave_sum_dpp(acc);
     if (lane == 0) {
         const uint64_t o = (uint64_t)tok * L.H + r;
         A.out[o] = (A.xres ? A.xres[o] : 0.0f) + tot;
     }
+}
+
+template <int NBI, int NBS, int KC>
+__global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
+    const LayerDev &L = A.L;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tiles_h = (L.H + 3) / 4;
+    const uint32_t tok = blockIdx.x / tiles_h, tile = blockIdx.x - tok * tiles_h;
+    const uint32_t r = tile * 4 + wave;
+    if (r >= L.H || tok >= (uint32_t)A.S) return;
+    cz_down_row<NBI, NBS, KC>(A, tok, r, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -620,11 +663,12 @@ __device__ inline float cz_dot_fp8_strided(const uint8_t *__restrict__ w, const 
     return acc;
 }
 
+template <int M>
 __global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xn = A.rms ? A.xn : A.x;
-    const UpItem it = cz_up_item(A, 4, xn);
+    const UpItem it = cz_up_item<M>(A, 4, xn);
     const uint32_t r = it.tile * 4 + wave;
     if (r >= it.rows) return;
     const float *xs = xn + (uint64_t)it.tok * L.H;
