@@ -51,6 +51,7 @@ SIGNATURES = {
     "colizig_hip_layer_init": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(Dims), vp]),
     "colizig_hip_expert_load": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp]),
     "colizig_hip_layer_set_shared": (ctypes.c_int, [ctypes.c_uint32, vp, vp, vp, vp, vp, vp, vp]),
+    "colizig_hip_layer_set_router_bias": (ctypes.c_int, [ctypes.c_uint32, vp]),
     "colizig_hip_moe_forward": (ctypes.c_int, [ctypes.c_uint32, vp, ctypes.c_int, vp, vp, vp]),
     "colizig_hip_moe_forward_dev": (ctypes.c_int, [ctypes.c_uint32, vp, ctypes.c_int, vp, vp, vp, vp]),
     "colizig_hip_chain_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,

@@ -5,7 +5,7 @@
 // stream at default priority.  Every entry point saves/restores the host
 // MXCSR (colizig_cuda.cu:22-29): the GPU runtime must not leak FTZ/DAZ into
 // the engine's CPU float math.
-#include "cz_kernels.h"
+#include "cz_grouped.h"
 #include "colizig_hip.h"
 
 #include <xmmintrin.h>
@@ -48,6 +48,7 @@ struct LayerHost {
     uint8_t *sw = nullptr;
     float *ss = nullptr;
     float *shg = nullptr;
+    float *rbias = nullptr;  // optional router bias [E]
     std::vector<uint8_t> loaded;
     uint32_t nloaded = 0;
     bool shared_set = false;
@@ -76,6 +77,7 @@ struct LayerHost {
         L.sw = sw;
         L.ss = ss;
         L.sh_gate = shg;
+        L.router_bias = rbias;
         return L;
     }
 };
@@ -88,6 +90,12 @@ struct Work {
     uint32_t *idx = nullptr;
     size_t cap_xin = 0, cap_out = 0, cap_xn = 0, cap_logits = 0, cap_idx = 0, cap_gates = 0, cap_sgate = 0,
            cap_h = 0, cap_hs = 0;
+    // grouped regime
+    uint32_t *counts = nullptr, *offsets = nullptr, *sorted_slot = nullptr, *slot_pos = nullptr,
+             *tok_order = nullptr, *tile_expert = nullptr, *tile_row0 = nullptr, *ntiles = nullptr;
+    float *o = nullptr, *os = nullptr;
+    size_t cap_counts = 0, cap_offsets = 0, cap_sorted = 0, cap_slot_pos = 0, cap_tok_order = 0, cap_tiles = 0,
+           cap_tiles2 = 0, cap_ntiles = 0, cap_o = 0, cap_os = 0;
 };
 
 struct Ctx {
@@ -183,8 +191,39 @@ int ensure_work(const colizig_dims &d, int S) {
     return 0;
 }
 
+// Upper bound on the M-tiles of the grouped GEMMs: sum_e ceil(n_e/32) <=
+// S*K/32 + min(E, S*K).
+uint32_t grouped_max_tiles(const colizig_dims &d, int S) {
+    const uint32_t sk = (uint32_t)S * d.topk;
+    return sk / CZ_GG_M + std::min(d.experts, sk) + 1;
+}
+
+int ensure_work_grouped(const colizig_dims &d, int S) {
+    Work &w = g.work;
+    const size_t s = (size_t)S, sk = s * d.topk, mt = grouped_max_tiles(d, S);
+    if (grow(&w.counts, &w.cap_counts, (size_t)d.experts) || grow(&w.offsets, &w.cap_offsets, (size_t)d.experts + 1) ||
+        grow(&w.sorted_slot, &w.cap_sorted, sk) || grow(&w.slot_pos, &w.cap_slot_pos, sk) ||
+        grow(&w.tok_order, &w.cap_tok_order, sk) || grow(&w.tile_expert, &w.cap_tiles, mt) ||
+        grow(&w.tile_row0, &w.cap_tiles2, mt) || grow(&w.ntiles, &w.cap_ntiles, (size_t)1) ||
+        grow(&w.o, &w.cap_o, sk * d.hidden) || grow(&w.os, &w.cap_os, std::max<size_t>(1, s * d.hidden))) {
+        snprintf(g_err, sizeof g_err, "grouped scratch allocation failed (S=%d)", S);
+        return -2;
+    }
+    return 0;
+}
+
+// The grouped (dispatch + MFMA) regime serves S >= kGroupedMinTokens when the
+// shapes tile by 128 and the slots fit the dispatch workgroup.
+constexpr int kGroupedMinTokens = 16;
+
+bool grouped_ok(const colizig_dims &d, int S) {
+    return S >= kGroupedMinTokens && d.hidden % 128 == 0 && d.inter % 128 == 0 && d.shared_inter % 128 == 0 &&
+           (size_t)S * d.topk <= CZ_DISPATCH_MAX;
+}
+
 void free_layer(LayerHost &L) {
-    for (void *p : {(void *)L.router, (void *)L.ew, (void *)L.es, (void *)L.sw, (void *)L.ss, (void *)L.shg})
+    for (void *p : {(void *)L.router, (void *)L.ew, (void *)L.es, (void *)L.sw, (void *)L.ss, (void *)L.shg,
+                    (void *)L.rbias})
         if (p) (void)hipFree(p);
     L = LayerHost{};
 }
@@ -329,8 +368,123 @@ int launch_step(const StepArgs &A, hipStream_t st, int which = kAll) {
     return 0;
 }
 
+// Grouped regime: router logits (as in decode), per-token routing, dispatch,
+// grouped gate/up and down GEMMs (routed experts, then the shared expert as
+// a dense problem), combine.
+template <int M>
+void launch_route_tokens(const GroupArgs &G, hipStream_t st) {
+    k_route_tokens<M><<<(G.S + 3) / 4, 256, 0, st>>>(G);
+}
+
+int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                   float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+    const StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
+    const LayerDev &L = A.L;
+    Work &w = g.work;
+    launch_router(A, st);
+    GroupArgs G{};
+    G.L = L;
+    G.S = S;
+    G.xn = rms ? w.xn : x;
+    G.logits = w.logits;
+    G.idx = w.idx;
+    G.gates = w.gates;
+    G.sgate = w.sgate;
+    G.idx_trace = idx_trace;
+    G.gates_trace = gates_trace;
+    G.counts = w.counts;
+    G.offsets = w.offsets;
+    G.sorted_slot = w.sorted_slot;
+    G.slot_pos = w.slot_pos;
+    G.tok_order = w.tok_order;
+    G.tile_expert = w.tile_expert;
+    G.tile_row0 = w.tile_row0;
+    G.ntiles = w.ntiles;
+    G.max_tiles = grouped_max_tiles(Lh.d, S);
+    G.h = w.h;
+    G.o = w.o;
+    G.hs = w.hs;
+    G.os = w.os;
+    G.xres = xres;
+    G.out = out;
+    switch (cz_route_groups(L.E)) {
+        case 1: launch_route_tokens<1>(G, st); break;
+        case 2: launch_route_tokens<2>(G, st); break;
+        case 4: launch_route_tokens<4>(G, st); break;
+        case 8: launch_route_tokens<8>(G, st); break;
+        default: launch_route_tokens<16>(G, st); break;
+    }
+    k_dispatch<<<1, 1024, 0, st>>>(G);
+    const uint32_t mts = (uint32_t)(S + CZ_GG_M - 1) / CZ_GG_M;
+    // gate/up
+    GGProblem P{};
+    P.w0 = L.ew;
+    P.s0 = L.es;
+    P.w_stride = L.ew_stride;
+    P.s_stride = L.es_stride;
+    P.w1_off = (uint64_t)L.I * L.H;
+    P.s1_off = (uint64_t)L.nbI * L.nbH;
+    P.N = L.I;
+    P.Kd = L.H;
+    P.nbK = L.nbH;
+    P.a = G.xn;
+    P.c = w.h;
+    P.routed = 1;
+    k_gg<GG_GATEUP><<<G.max_tiles * (L.I / CZ_GG_N), 256, 0, st>>>(G, P);
+    if (L.SI) {
+        GGProblem Q = P;
+        Q.w0 = L.sw;
+        Q.s0 = L.ss;
+        Q.w_stride = 0;
+        Q.s_stride = 0;
+        Q.w1_off = (uint64_t)L.SI * L.H;
+        Q.s1_off = (uint64_t)L.nbSI * L.nbH;
+        Q.N = L.SI;
+        Q.c = w.hs;
+        Q.routed = 0;
+        Q.rows_total = (uint32_t)S;
+        k_gg<GG_GATEUP><<<mts * (L.SI / CZ_GG_N), 256, 0, st>>>(G, Q);
+    }
+    // down
+    GGProblem D{};
+    D.w0 = L.ew + 2ull * L.I * L.H;
+    D.s0 = L.es + 2ull * L.nbI * L.nbH;
+    D.w_stride = L.ew_stride;
+    D.s_stride = L.es_stride;
+    D.N = L.H;
+    D.Kd = L.I;
+    D.nbK = L.nbI;
+    D.a = w.h;
+    D.c = w.o;
+    D.routed = 1;
+    k_gg<GG_DOWN><<<G.max_tiles * (L.H / CZ_GG_N), 256, 0, st>>>(G, D);
+    if (L.SI) {
+        GGProblem Q = D;
+        Q.w0 = L.sw + 2ull * L.SI * L.H;
+        Q.s0 = L.ss + 2ull * L.nbSI * L.nbH;
+        Q.w_stride = 0;
+        Q.s_stride = 0;
+        Q.Kd = L.SI;
+        Q.nbK = L.nbSI;
+        Q.a = w.hs;
+        Q.c = w.os;
+        Q.routed = 0;
+        Q.rows_total = (uint32_t)S;
+        k_gg<GG_DOWN><<<mts * (L.H / CZ_GG_N), 256, 0, st>>>(G, Q);
+    }
+    k_combine<<<dim3((L.H + 255) / 256, S), 256, 0, st>>>(G);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "grouped launch: %s", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
 int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
                  float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+    if (grouped_ok(Lh.d, S))
+        return launch_grouped(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace, st);
     return launch_step(step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace), st);
 }
 
@@ -433,7 +587,9 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (g.h_stage) (void)hipHostFree(g.h_stage);
     Work &w = g.work;
     for (void *p : {(void *)w.xin, (void *)w.out, (void *)w.xn, (void *)w.logits, (void *)w.gates,
-                    (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx})
+                    (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx, (void *)w.counts, (void *)w.offsets,
+                    (void *)w.sorted_slot, (void *)w.slot_pos, (void *)w.tok_order, (void *)w.tile_expert,
+                    (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     (void)hipStreamDestroy(g.stream);
@@ -663,6 +819,25 @@ extern "C" int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char 
     return 0;
 }
 
+extern "C" int colizig_hip_layer_set_router_bias(uint32_t layer, const float *bias) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L) return -1;
+    (void)hipStreamSynchronize(g.stream);
+    if (!bias) {
+        if (L->rbias) (void)hipFree(L->rbias);
+        L->rbias = nullptr;
+        return 0;
+    }
+    if (!L->rbias && hipMalloc(&L->rbias, (size_t)L->d.experts * sizeof(float)) != hipSuccess) {
+        L->rbias = nullptr;
+        return -2;
+    }
+    CZ_CHECK(hipMemcpy(L->rbias, bias, (size_t)L->d.experts * sizeof(float), hipMemcpyHostToDevice), -3);
+    return 0;
+}
+
 extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, int S, float *out_dev,
                                            uint32_t *idx_dev, float *gates_dev, void *stream) {
     CsrGuard csr;
@@ -672,6 +847,7 @@ extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, i
     int rc = check_layer_ready(L, layer);
     if (rc) return rc;
     if ((rc = ensure_work(L->d, S))) return rc;
+    if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     return launch_layer(*L, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, idx_dev, gates_dev, pick_stream(stream));
 }
 
@@ -684,6 +860,7 @@ extern "C" int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, fl
     int rc = check_layer_ready(L, layer);
     if (rc) return rc;
     if ((rc = ensure_work(L->d, S))) return rc;
+    if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     const size_t xb = (size_t)S * L->d.hidden * sizeof(float);
     const size_t kb = (size_t)S * L->d.topk * sizeof(float);
     if (ensure_host(xb + 2 * kb)) return -2;
@@ -709,6 +886,7 @@ static int chain_enqueue(uint32_t layer0, uint32_t nlayers, float *x_dev, int S,
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
         if ((rc = ensure_work(L->d, S))) return rc;
+        if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
@@ -740,6 +918,7 @@ extern "C" int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlay
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
         if ((rc = ensure_work(L->d, S))) return rc;
+        if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
     CZ_CHECK(hipStreamSynchronize(g.stream), -4);
     hipGraph_t graph = nullptr;
@@ -938,6 +1117,7 @@ extern "C" int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers,
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
         if ((rc = ensure_work(L->d, S))) return rc;
+        if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
     std::vector<StepArgs> args;
     for (uint32_t l = 0; l < nlayers; ++l) {

@@ -35,6 +35,7 @@ struct LayerDev {
     const uint8_t *sw;     // shared weights (gate|up|down) or null
     const float *ss;       // shared scales (gate|up|down)
     const float *sh_gate;  // [H]
+    const float *router_bias;  // [E] added to each logit, or null (workload shaping only)
 };
 
 #define CZ_ROUTER_TT 4    // most tokens per router tile
@@ -257,7 +258,8 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < NS; ++i) acc = __builtin_fmaf(xs[32 * i], w[i], acc);
-        const float lg = cz_router_combine(acc, j, hb);
+        float lg = cz_router_combine(acc, j, hb);
+        if (A.L.router_bias) lg = lg + A.L.router_bias[ec];
         if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
     }
 }
@@ -275,7 +277,8 @@ __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
     __syncthreads();
     const float *wr = A.L.router + (uint64_t)ec * H;
     for (uint32_t t = 0; t < nt; ++t) {
-        const float lg = cz_router_dot(smem + t * H, wr, H, j, hb);
+        float lg = cz_router_dot(smem + t * H, wr, H, j, hb);
+        if (A.L.router_bias) lg = lg + A.L.router_bias[ec];
         if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
     }
 }

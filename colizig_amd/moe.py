@@ -152,6 +152,12 @@ class Layer:
         _check("colizig_hip_layer_set_shared",
                _lib.hip().colizig_hip_layer_set_shared(self.layer, *[_p(a) for a in arrs]))
 
+    def set_router_bias(self, bias: np.ndarray | None) -> None:
+        """Optional per-expert logit bias (workload shaping; None clears it)."""
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        assert b is None or b.shape == (self.d.experts,)
+        _check("colizig_hip_layer_set_router_bias", _lib.hip().colizig_hip_layer_set_router_bias(self.layer, _p(b)))
+
     def synth(self, seed: int, std_w: float = 0.02, std_router: float = 0.02) -> None:
         _check("colizig_hip_layer_synth", _lib.hip().colizig_hip_layer_synth(self.layer, seed, std_w, std_router))
 
@@ -203,6 +209,8 @@ def register_layer(layer: int, host: dict) -> Layer:
     if host.get("shared") is not None:
         s = host["shared"]
         L.set_shared(s["gate_w"], s["gate_s"], s["up_w"], s["up_s"], s["down_w"], s["down_s"], s["sh_gate"])
+    if host.get("router_bias") is not None:
+        L.set_router_bias(host["router_bias"])
     return L
 
 

@@ -94,3 +94,15 @@ def make_layer(hidden: int, experts: int, topk: int, inter: int, shared_inter: i
 def hidden_states(S: int, hidden: int, seed: int) -> np.ndarray:
     """x ~ N(0,1) f32 [S, hidden]"""
     return np.random.default_rng(seed).normal(0.0, 1.0, size=(S, hidden)).astype(np.float32)
+
+
+def zipf_router_bias(E: int, s: float, seed: int) -> np.ndarray:
+    """Per-expert router bias that makes expert popularity Zipf(s): p_e is
+    proportional to rank^-s over a seeded permutation of the experts, and
+    b_e = ln(p_e) - mean(ln p).  Added to the logits, it multiplies each
+    expert's softmax weight by p_e (up to a common factor)."""
+    rng = np.random.default_rng(seed)
+    ranks = np.empty(E, np.float64)
+    ranks[rng.permutation(E)] = np.arange(1, E + 1, dtype=np.float64)
+    lp = -s * np.log(ranks)
+    return (lp - lp.mean()).astype(np.float32)

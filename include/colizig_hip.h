@@ -107,9 +107,21 @@ int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char *gate_w, co
                                  const unsigned char *up_w, const float *up_s, const unsigned char *down_w,
                                  const float *down_s, const float *sh_gate);
 
+/* Optional per-expert router bias: logits[e] = dot(router[e], x) + bias[e]
+ * (one f32 add after the dot).  bias[E] f32, NULL clears it.  No counterpart
+ * in the reference, whose route has no bias term (moe.zig:435-463): a
+ * workload-shaping hook that skews routing (e.g. Zipf-distributed expert
+ * popularity) for prefill and streaming-tier benchmarks. */
+int colizig_hip_layer_set_router_bias(uint32_t layer, const float *bias);
+
 /* moe.forward (moe.zig:409-426) on host pointers, synchronous:
  * out[S*H] = MoE(x[S*H]).  routed_idx[S*K] / routed_gates[S*K] (nullable)
  * receive each token's top-k expert ids and gates in selection order.
+ * S = 1..15 runs the decode kernels (one GEMV per token and slot, combine in
+ * top-k order, as forwardDense); S >= 16 with H, I, SI multiples of 128 runs
+ * the grouped regime (forwardGrouped, moe.zig:597-665): dispatch of the S*K
+ * slots into per-expert row lists, grouped MFMA GEMMs, combine with the
+ * shared expert first and the experts in ascending id order.
  * 0 ok; -1 bad args; -2 alloc; -3 H2D; -4 launch; -5 D2H/fault;
  * -6 layer not registered or experts missing. */
 int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, uint32_t *routed_idx,

@@ -575,6 +575,10 @@ float czo_silu(float x) { return x * czo_sigmoid(x); }
 /* tensors.zig:114-119 NativeMatrix(f32).matmul -> matmul.zig:21-33 (S=1) */
 void czo_router_logits(const czo_layer *L, const float *xs, float *logits) {
     czo_matmul_f32(logits, xs, L->router, 1, L->d.hidden, L->d.experts);
+    /* optional per-expert bias, one f32 add after the dot: a workload-shaping
+     * extension (skewed routing); the reference's route has no bias term */
+    if (L->router_bias)
+        for (uint32_t e = 0; e < L->d.experts; ++e) logits[e] = logits[e] + L->router_bias[e];
 }
 
 /* moe.zig:435-463 route */

@@ -66,6 +66,7 @@ typedef struct czo_layer {
     czo_fp8mat sh_up_proj;     /* [shared_inter, hidden] */
     czo_fp8mat sh_down_proj;   /* [hidden, shared_inter] */
     const float *sh_gate;      /* [hidden] f32 */
+    const float *router_bias;  /* [experts] added to each logit, or NULL (the reference: none) */
 } czo_layer;
 
 /* ---- fp8.zig ---------------------------------------------------------- */

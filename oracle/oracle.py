@@ -32,7 +32,8 @@ class CExpert(ctypes.Structure):
 
 class CLayer(ctypes.Structure):
     _fields_ = [("d", CDims), ("router", vp), ("experts", ctypes.POINTER(CExpert)),
-                ("sh_gate_proj", CMat), ("sh_up_proj", CMat), ("sh_down_proj", CMat), ("sh_gate", vp)]
+                ("sh_gate_proj", CMat), ("sh_up_proj", CMat), ("sh_down_proj", CMat), ("sh_gate", vp),
+                ("router_bias", vp)]
 
 
 class CCacheStats(ctypes.Structure):
@@ -127,6 +128,9 @@ class OracleLayer:
             L.sh_up_proj = _mat(s["up_w"], s["up_s"])
             L.sh_down_proj = _mat(s["down_w"], s["down_s"])
             L.sh_gate = _p(s["sh_gate"])
+        if host.get("router_bias") is not None:
+            self.router_bias = np.ascontiguousarray(host["router_bias"], dtype=np.float32)
+            L.router_bias = _p(self.router_bias)
         self.c = L
         self.d = d
 

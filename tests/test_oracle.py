@@ -397,3 +397,34 @@ def test_chunk_bounds(oracle_lib):
         assert lib.czo_chunk_bounds(5, 1 << 20, _p(buf), 64) == 5  # tasks capped at n
     finally:
         lib.czo_parallel_disable()
+
+
+def test_router_bias_is_one_add_after_the_dot(oracle_lib):
+    """The optional router bias (workload shaping) adds bias[e] to each logit
+    with one f32 add after the dotF32 logit; without it routing is the
+    reference's."""
+    from colizig_amd import synth
+    host = synth.make_layer(256, 32, 4, 128, 0, True, seed=3)
+    plain = oracle_lib.OracleLayer(host)
+    bias = synth.zipf_router_bias(32, 1.1, seed=1)
+    biased = oracle_lib.OracleLayer(dict(host, router_bias=bias))
+    x = synth.hidden_states(1, 256, seed=4)[0]
+    want = (plain.router_logits(x) + bias).astype(np.float32)
+    assert np.array_equal(biased.router_logits(x).view(np.uint32), want.view(np.uint32))
+    # the biased route is the reference route on the biased logits: brute force
+    idx, _, _ = biased.route(x)
+    v = np.exp(want.astype(np.float64) - want.max())
+    order = sorted(range(32), key=lambda e: (-v[e], e))[:4]
+    assert list(idx) == order
+
+
+def test_zipf_bias_skews_popularity(oracle_lib):
+    """Zipf(1.1) bias: over many tokens the most popular expert is picked far
+    more often than the median one (a property of the workload generator)."""
+    from colizig_amd import synth
+    host = synth.make_layer(128, 64, 4, 128, 0, True, seed=8)
+    host["router_bias"] = synth.zipf_router_bias(64, 1.1, seed=2)
+    O = oracle_lib.OracleLayer(host)
+    _, idx, _ = O.forward(synth.hidden_states(256, 128, seed=8))
+    c = np.bincount(idx.ravel(), minlength=64)
+    assert c.max() > 4 * max(np.median(c), 1)
