@@ -73,6 +73,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                    help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
+                         "512 tokens with Zipf(1.1) routing skew (grouped regime)")
+    ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -82,6 +86,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.workload == "prefill":
+        prefill_bench(args)
         return
 
     from colizig_amd import _lib, moe
@@ -187,6 +194,75 @@ def main():
         "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
         "parity": parity,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def prefill_bench(args) -> None:
+    """Qwen3-30B-A3B MoE shapes at prefill: 48 chained layers, `tokens` tokens
+    per step, each layer's routing skewed Zipf(1.1) by a per-expert logit bias
+    over a seeded permutation.  Runs the grouped regime (dispatch + grouped
+    MFMA GEMMs).  Algorithmic bytes per step: every expert a layer's routing
+    touches, read once, + routers + activations."""
+    from colizig_amd import _lib, moe, synth
+    c = dict(CONFIG)
+    c.update(workload="qwen3-30b-a3b-moe-prefill-zipf1.1", batch=args.tokens, zipf_s=1.1)
+    c["layers"] = args.layers
+    H, E, K, I, NL, S = c["hidden"], c["experts"], c["topk"], c["inter"], c["layers"], args.tokens
+    name = moe.init()
+    log(f"device: {name}")
+    hip = _lib.hip()
+    d = moe.dims(H, E, K, I, 0, True)
+    zero_router = np.zeros((E, H), np.float32)
+    for l in range(NL):
+        L = moe.Layer.load(l, d, zero_router)
+        L.synth(seed=c["seed"] * 1000003 + l)
+        L.set_router_bias(synth.zipf_router_bias(E, 1.1, seed=7919 * l + 1))
+    x0 = np.random.default_rng(c["seed"]).normal(0.0, 1.0, size=(S, H)).astype(np.float32)
+    xb = moe.DeviceBuffer(x0.nbytes)
+    eps = 1e-6
+    # one traced pass: the experts each layer touches
+    idx_t = moe.DeviceBuffer(NL * S * K * 4)
+    xb.upload(x0)
+    assert hip.colizig_hip_chain_decode(0, NL, xb.ptr, S, eps, None, idx_t.ptr, None, None) == 0, _lib.last_error()
+    assert hip.colizig_hip_sync() == 0
+    idx = idx_t.download(np.empty((NL, S, K), np.uint32))
+    touched = [int(np.unique(idx[l]).size) for l in range(NL)]
+    hottest = [int(np.bincount(idx[l].ravel(), minlength=E).max()) for l in range(NL)]
+    per_expert = 3 * H * I + 4 * (2 * nblk(I) * nblk(H) + nblk(H) * nblk(I))
+    step_bytes = sum(t * per_expert for t in touched) + NL * (E * H * 4 + 2 * S * H * 4)
+    step_flops = NL * S * K * 2 * 3 * H * I
+    xb.upload(x0)
+    gh = hip.colizig_hip_chain_graph_create(0, NL, xb.ptr, S, eps)
+    if gh <= 0:
+        raise RuntimeError(f"graph capture failed: {_lib.last_error()}")
+    for _ in range(args.warmup):
+        assert hip.colizig_hip_graph_launch(gh, None) == 0
+    assert hip.colizig_hip_sync() == 0
+    ev0, ev1 = hip.colizig_hip_event_create(), hip.colizig_hip_event_create()
+    hip.colizig_hip_event_record(ev0, None)
+    for _ in range(args.steps):
+        hip.colizig_hip_graph_launch(gh, None)
+    hip.colizig_hip_event_record(ev1, None)
+    assert hip.colizig_hip_sync() == 0
+    ms = hip.colizig_hip_event_elapsed_ms(ev0, ev1) / args.steps
+    tok_s = S * 1000.0 / ms
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"prefill: {S} tokens x {NL} layers in {ms:.3f} ms ({tok_s:.0f} tok/s); experts touched per layer "
+        f"{min(touched)}..{max(touched)}, hottest expert {max(hottest)} of {S} tokens; {gbs:.0f} GB/s; "
+        f"{step_flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
+    line = {
+        "metric": "MoE prefill tok/s (512-token step, Zipf(1.1) routing), Qwen3-30B-A3B shape, 1 MI355X",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "e4m3-weights/f16x2-activations/f32-accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights generated in HBM, N(0,1) hidden states)",
+        "config": {**c, "parallelism": "none (1 GPU)", "global_batch": S, "seq_len": S},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole step",
+                     "bytes_per_step": step_bytes},
+        "mfma_tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
+        "experts_touched_per_layer": [min(touched), max(touched)],
     }
     print(json.dumps(line), flush=True)
 

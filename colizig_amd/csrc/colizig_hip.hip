@@ -191,6 +191,10 @@ int ensure_work(const colizig_dims &d, int S) {
     return 0;
 }
 
+// The grouped (dispatch + MFMA) regime serves S >= kGroupedMinTokens when the
+// shapes tile by 128 and the slots fit the dispatch workgroup.
+constexpr int kGroupedMinTokens = 16;
+
 // Upper bound on the M-tiles of the grouped GEMMs: sum_e ceil(n_e/32) <=
 // S*K/32 + min(E, S*K).
 uint32_t grouped_max_tiles(const colizig_dims &d, int S) {
@@ -212,9 +216,6 @@ int ensure_work_grouped(const colizig_dims &d, int S) {
     return 0;
 }
 
-// The grouped (dispatch + MFMA) regime serves S >= kGroupedMinTokens when the
-// shapes tile by 128 and the slots fit the dispatch workgroup.
-constexpr int kGroupedMinTokens = 16;
 
 bool grouped_ok(const colizig_dims &d, int S) {
     return S >= kGroupedMinTokens && d.hidden % 128 == 0 && d.inter % 128 == 0 && d.shared_inter % 128 == 0 &&
@@ -243,6 +244,10 @@ enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
 
 void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
+    if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: 16-token tiles
+        k_router_tiled<<<dim3((L.E + 7) / 8, (A.S + CZ_RT_TOK - 1) / CZ_RT_TOK), 256, 0, st>>>(A);
+        return;
+    }
     const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);
     const size_t lds = (size_t)A.tt * L.H * sizeof(float);
     switch ((L.H % 32) ? 0u : L.H / 32) {
@@ -371,6 +376,10 @@ int launch_step(const StepArgs &A, hipStream_t st, int which = kAll) {
 // Grouped regime: router logits (as in decode), per-token routing, dispatch,
 // grouped gate/up and down GEMMs (routed experts, then the shared expert as
 // a dense problem), combine.
+// grid of a grouped GEMM: M-tiles rounded up to whole groups of 8 (one per
+// XCD) times the N-tiles; workgroups past the real M-tiles exit
+uint32_t gg_blocks(uint32_t mtiles, uint32_t N) { return ((mtiles + 7) / 8) * 8 * (N / CZ_GG_N); }
+
 template <int M>
 void launch_route_tokens(const GroupArgs &G, hipStream_t st) {
     k_route_tokens<M><<<(G.S + 3) / 4, 256, 0, st>>>(G);
@@ -430,7 +439,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     P.a = G.xn;
     P.c = w.h;
     P.routed = 1;
-    k_gg<GG_GATEUP><<<G.max_tiles * (L.I / CZ_GG_N), 256, 0, st>>>(G, P);
+    k_gg<GG_GATEUP><<<gg_blocks(G.max_tiles, L.I), 256, 0, st>>>(G, P);
     if (L.SI) {
         GGProblem Q = P;
         Q.w0 = L.sw;
@@ -443,7 +452,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.c = w.hs;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
-        k_gg<GG_GATEUP><<<mts * (L.SI / CZ_GG_N), 256, 0, st>>>(G, Q);
+        k_gg<GG_GATEUP><<<gg_blocks(mts, L.SI), 256, 0, st>>>(G, Q);
     }
     // down
     GGProblem D{};
@@ -457,7 +466,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     D.a = w.h;
     D.c = w.o;
     D.routed = 1;
-    k_gg<GG_DOWN><<<G.max_tiles * (L.H / CZ_GG_N), 256, 0, st>>>(G, D);
+    k_gg<GG_DOWN><<<gg_blocks(G.max_tiles, L.H), 256, 0, st>>>(G, D);
     if (L.SI) {
         GGProblem Q = D;
         Q.w0 = L.sw + 2ull * L.SI * L.H;
@@ -470,7 +479,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.c = w.os;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
-        k_gg<GG_DOWN><<<mts * (L.H / CZ_GG_N), 256, 0, st>>>(G, Q);
+        k_gg<GG_DOWN><<<gg_blocks(mts, L.H), 256, 0, st>>>(G, Q);
     }
     k_combine<<<dim3((L.H + 255) / 256, S), 256, 0, st>>>(G);
     const hipError_t e = hipGetLastError();

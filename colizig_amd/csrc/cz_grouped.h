@@ -76,13 +76,20 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     const uint32_t t = blockIdx.x * 4 + wave;
     if (t >= (uint32_t)G.S) return;  // wave-uniform
     cz_route_wave_m<M>(G.logits + (uint64_t)t * L.E, L.E, L.K, L.norm_topk, s_idx[wave], s_gate[wave]);
+    uint32_t my_e = 0xffffffffu;
     if (lane < L.K) {  // lane z reads back the entry it wrote
         const uint64_t o = (uint64_t)t * L.K + lane;
-        G.idx[o] = s_idx[wave][lane];
+        my_e = s_idx[wave][lane];
+        G.idx[o] = my_e;
         G.gates[o] = s_gate[wave][lane];
-        if (G.idx_trace) G.idx_trace[o] = s_idx[wave][lane];
+        if (G.idx_trace) G.idx_trace[o] = my_e;
         if (G.gates_trace) G.gates_trace[o] = s_gate[wave][lane];
     }
+    // the token's slots in ascending expert id (the K ids are distinct): lane
+    // z's rank is the number of the token's experts below its own
+    uint32_t rank = 0;
+    for (uint32_t q = 0; q < L.K; ++q) rank += (uint32_t)__builtin_amdgcn_readlane((int)my_e, q) < my_e ? 1u : 0u;
+    if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + lane;
     if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         const float *xs = G.xn + (uint64_t)t * L.H;
         float d = 0.0f;
@@ -96,98 +103,125 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
 }
 
 // ---------------------------------------------------------------------------
-// dispatch: one workgroup of 1024 threads, the S*K slot ids in LDS
-// (S*K <= CZ_DISPATCH_MAX).  Stable: within an expert, rows keep slot order.
+// dispatch: one workgroup of 1024 threads (16 waves) over the S*K slot ids
+// (S*K <= CZ_DISPATCH_MAX, E <= CZ_MAX_E).  Counts by LDS integer atomics
+// (order-independent), offsets by one prefix, then a stable placement in
+// rounds of 1024 slots: inside a wave, equal ids are ranked by ballot in lane
+// order; across the round's waves, per-expert running bases are prefixed in
+// wave order.  Within an expert, rows keep slot order.
 // ---------------------------------------------------------------------------
 #define CZ_DISPATCH_MAX 8192
 
 __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
     const LayerDev &L = G.L;
-    const uint32_t E = L.E, K = L.K, SK = (uint32_t)G.S * L.K;
-    __shared__ uint32_t s_slot_e[CZ_DISPATCH_MAX];
+    const uint32_t E = L.E, SK = (uint32_t)G.S * L.K;
+    __shared__ uint16_t s_slot_e[CZ_DISPATCH_MAX];
+    __shared__ uint16_t s_wcnt[16][CZ_MAX_E];  // this round's count per (wave, expert), then its base
     __shared__ uint32_t s_cnt[CZ_MAX_E];
     __shared__ uint32_t s_off[CZ_MAX_E + 1];
-    __shared__ uint32_t s_tile0[CZ_MAX_E + 1];
-    const uint32_t tid = threadIdx.x, lane = cz_lane(), wave = tid >> 6, nwaves = blockDim.x >> 6;
-    for (uint32_t i = tid; i < E; i += blockDim.x) s_cnt[i] = 0;
-    for (uint32_t i = tid; i < SK; i += blockDim.x) s_slot_e[i] = min(G.idx[i], E - 1);
+    __shared__ uint32_t s_run[CZ_MAX_E];       // rows placed so far per expert
+    const uint32_t tid = threadIdx.x, lane = cz_lane(), wave = tid >> 6;
+    for (uint32_t i = tid; i < E; i += blockDim.x) {
+        s_cnt[i] = 0;
+        s_run[i] = 0;
+    }
+    for (uint32_t i = tid; i < 16 * CZ_MAX_E; i += blockDim.x) (&s_wcnt[0][0])[i] = 0;
+    for (uint32_t i = tid; i < SK; i += blockDim.x) s_slot_e[i] = (uint16_t)min(G.idx[i], E - 1);
     __syncthreads();
-    // 1. counts (integer atomics: order-independent)
     for (uint32_t i = tid; i < SK; i += blockDim.x) atomicAdd(&s_cnt[s_slot_e[i]], 1u);
     __syncthreads();
-    // 2. exclusive prefix over experts, and of their M-tile counts (one thread)
-    if (tid == 0) {
+    if (tid < 64) {  // one wave: exclusive prefix of counts and of M-tile counts
         uint32_t acc = 0, tacc = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            s_off[e] = acc;
-            s_tile0[e] = tacc;
-            acc += s_cnt[e];
-            tacc += (s_cnt[e] + CZ_GG_M - 1) / CZ_GG_M;
+        for (uint32_t e0 = 0; e0 < E; e0 += 64) {
+            const uint32_t e = e0 + lane;
+            const uint32_t c = e < E ? s_cnt[e] : 0u;
+            const uint32_t tc = (c + CZ_GG_M - 1) / CZ_GG_M;
+            // inclusive scans over the 64 lanes (shuffles; tiny)
+            uint32_t ic = c, it = tc;
+            for (uint32_t off = 1; off < 64; off <<= 1) {
+                const uint32_t a = __shfl_up(ic, off, 64), b = __shfl_up(it, off, 64);
+                if (lane >= off) { ic += a; it += b; }
+            }
+            if (e < E) {
+                s_off[e] = acc + ic - c;
+                const uint32_t tile0 = tacc + it - tc;
+                for (uint32_t k = 0; k < tc; ++k) {
+                    const uint32_t tile = tile0 + k;
+                    if (tile < G.max_tiles) {
+                        G.tile_expert[tile] = e;
+                        G.tile_row0[tile] = acc + ic - c + k * CZ_GG_M;
+                    }
+                }
+            }
+            acc += (uint32_t)__shfl(ic, 63, 64);
+            tacc += (uint32_t)__shfl(it, 63, 64);
         }
-        s_off[E] = acc;
-        s_tile0[E] = tacc;
-        G.ntiles[0] = min(tacc, G.max_tiles);
+        if (lane == 0) {
+            s_off[E] = acc;
+            G.ntiles[0] = min(tacc, G.max_tiles);
+        }
     }
     __syncthreads();
     for (uint32_t e = tid; e <= E; e += blockDim.x) {
         G.offsets[e] = s_off[e];
         if (e < E) G.counts[e] = s_cnt[e];
     }
-    // 3. stable placement: wave w owns experts w, w + nwaves, ...; a ballot over
-    //    each 64-slot chunk ranks equal ids in slot order
-    for (uint32_t e = wave; e < E; e += nwaves) {
-        if (s_cnt[e] == 0) continue;  // wave-uniform
-        uint32_t base = s_off[e];
-        for (uint32_t c0 = 0; c0 < SK; c0 += 64) {
-            const uint32_t i = c0 + lane;
-            const bool hit = i < SK && s_slot_e[i] == e;
-            const uint64_t m = __ballot(hit);
-            if (hit) {
-                const uint32_t pos = base + (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
-                G.sorted_slot[pos] = i;
-                G.slot_pos[i] = pos;
+    for (uint32_t r0 = 0; r0 < SK; r0 += blockDim.x) {
+        const uint32_t i = r0 + tid;
+        const bool valid = i < SK;
+        const uint32_t e = valid ? s_slot_e[i] : 0u;
+        // rank among the wave's equal ids, and the wave's count per id
+        uint32_t rank = 0;
+        bool pending = valid;
+        while (__ballot(pending)) {
+            const uint64_t pm = __ballot(pending);
+            const uint32_t leader = (uint32_t)__builtin_ctzll(pm);
+            const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)e, leader);
+            const uint64_t m = __ballot(pending && e == v);
+            if (pending && e == v) {
+                rank = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
+                pending = false;
             }
-            base += (uint32_t)__builtin_popcountll(m);
+            if (lane == leader) s_wcnt[wave][v] = (uint16_t)__builtin_popcountll(m);
         }
-        // 4. this expert's M-tiles
-        const uint32_t nt = (s_cnt[e] + CZ_GG_M - 1) / CZ_GG_M;
-        for (uint32_t k = lane; k < nt; k += 64) {
-            const uint32_t tile = s_tile0[e] + k;
-            if (tile < G.max_tiles) {
-                G.tile_expert[tile] = e;
-                G.tile_row0[tile] = s_off[e] + k * CZ_GG_M;
+        __syncthreads();
+        // per expert: bases of the round's waves in wave order
+        for (uint32_t x = tid; x < E; x += blockDim.x) {
+            uint32_t run = s_run[x];
+            for (uint32_t w = 0; w < 16; ++w) {
+                const uint32_t c = s_wcnt[w][x];
+                s_wcnt[w][x] = (uint16_t)run;  // this wave's base (fits: run < S*K <= 8192)
+                run += c;
             }
+            s_run[x] = run;
         }
-    }
-    // 5. each token's slots in ascending expert id (insertion sort of K)
-    for (uint32_t t = tid; t < (uint32_t)G.S; t += blockDim.x) {
-        uint32_t ord[CZ_MAX_K];
-        for (uint32_t z = 0; z < K; ++z) {
-            const uint32_t s = t * K + z, e = s_slot_e[s];
-            uint32_t j = z;
-            while (j > 0 && s_slot_e[ord[j - 1]] > e) { ord[j] = ord[j - 1]; --j; }
-            ord[j] = s;
+        __syncthreads();
+        if (valid) {
+            const uint32_t pos = s_off[e] + s_wcnt[wave][e] + rank;
+            G.sorted_slot[pos] = i;
+            G.slot_pos[i] = pos;
         }
-        for (uint32_t z = 0; z < K; ++z) G.tok_order[(uint64_t)t * K + z] = ord[z];
+        __syncthreads();
+        for (uint32_t x = tid; x < 16 * CZ_MAX_E; x += blockDim.x) (&s_wcnt[0][0])[x] = 0;
+        __syncthreads();
     }
 }
 
 // ---------------------------------------------------------------------------
 // grouped GEMM
 // ---------------------------------------------------------------------------
-// 8 E4M3 bytes (two dwords) -> 8 f16, exact (every E4M3 value is an f16)
+// 8 E4M3 bytes (two dwords) -> 8 f16, exact: every E4M3 value is an f16,
+// and gfx950's v_cvt_scalef32_pk_f16_fp8 with scale 1.0 converts two bytes
+// of a dword per instruction (word_sel picks bytes 0-1 or 2-3)
 __device__ inline cz_half8 cz_fp8x8_to_f16(uint32_t w0, uint32_t w1) {
-    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-    const cz_float2 a = cz_fp8x2_lo(w0), b = cz_fp8x2_hi(w0), c = cz_fp8x2_lo(w1), d = cz_fp8x2_hi(w1);
-    const fp16x2 p[4] = {__builtin_amdgcn_cvt_pkrtz(a.x, a.y), __builtin_amdgcn_cvt_pkrtz(b.x, b.y),
-                         __builtin_amdgcn_cvt_pkrtz(c.x, c.y), __builtin_amdgcn_cvt_pkrtz(d.x, d.y)};
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, false);
+    const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, true);
+    const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w1, 1.0f, false);
+    const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w1, 1.0f, true);
     cz_half8 r;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t bits = __builtin_bit_cast(uint32_t, p[q]);
-        r[2 * q] = __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
-        r[2 * q + 1] = __builtin_bit_cast(_Float16, (uint16_t)(bits >> 16));
-    }
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
     return r;
 }
 
@@ -218,8 +252,11 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
     __shared__ uint32_t s_rowdst[CZ_GG_M];  // C row index of each tile row
 
     const uint32_t lane = cz_lane(), wave = threadIdx.x >> 6, tid = threadIdx.x;
+    // XCD-aware order: workgroup b runs on XCD b % 8, so M-tile mt is pinned to
+    // XCD mt % 8 for all of its N-tiles and its A rows are read into one L2:
+    // b = ((mt / 8) * ntn + nt) * 8 + mt % 8
     const uint32_t ntn = P.N / CZ_GG_N;
-    const uint32_t mt = blockIdx.x / ntn, nt = blockIdx.x - mt * ntn;
+    const uint32_t grp = blockIdx.x >> 3, mt = (grp / ntn) * 8 + (blockIdx.x & 7), nt = grp % ntn;
     uint32_t e = 0, row0 = 0, rows = 0;
     if (P.routed) {
         if (mt >= G.ntiles[0]) return;  // block-uniform
@@ -269,24 +306,29 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
 
-    uint4 wreg[NMAT][4];
-    float4 areg[4];
-    auto load_kb = [&](uint32_t kb) {
+    // K blocks kb+1 and kb+2 are in flight while kb is multiplied: weights in
+    // registers (two sets), the A rows of kb+1 staged to LDS at the end of
+    // iteration kb (double-buffered LDS)
+    uint4 wA[NMAT][4], wB[NMAT][4];
+    float4 aA[4], aB[4];
+    auto load_w = [&](uint32_t kb, uint4 (&w)[NMAT][4]) {
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wreg[m][q] = ((const uint4 *)(wrow[m] + (uint64_t)kb * CZ_GG_KB))[q];
+            for (int q = 0; q < 4; ++q) w[m][q] = ((const uint4 *)(wrow[m] + (uint64_t)kb * CZ_GG_KB))[q];
+    };
+    auto load_a = [&](uint32_t kb, float4 (&a)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            areg[q] = arow ? ((const float4 *)(arow + (uint64_t)kb * CZ_GG_KB))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            a[q] = arow ? ((const float4 *)(arow + (uint64_t)kb * CZ_GG_KB))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     // f32 -> f16 hi + lo (hi = f16(v), lo = f16(v - hi)), two 16-byte LDS
     // stores per array
-    auto stage_a = [&](int buf) {
+    auto stage_a = [&](int buf, const float4 (&a)[4]) {
         cz_half8 hv[2], lv[2];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float v[4] = {areg[q].x, areg[q].y, areg[q].z, areg[q].w};
+            const float v[4] = {a[q].x, a[q].y, a[q].z, a[q].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const _Float16 h = (_Float16)v[j];
@@ -300,21 +342,30 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
         lo[0] = lv[0]; lo[1] = lv[1];
     };
 
-    const uint32_t nkb = P.Kd / CZ_GG_KB;
-    load_kb(0);
-    stage_a(0);
+    const uint32_t nkb = P.Kd / CZ_GG_KB;  // >= 1
+    load_w(0, wA);
+    load_a(0, aA);
+    if (nkb > 1) {
+        load_w(1, wB);
+        load_a(1, aB);
+    }
+    stage_a(0, aA);
     __syncthreads();
     for (uint32_t kb = 0; kb < nkb; ++kb) {
         const int buf = kb & 1;
+        // this block's weights leave wA; wA then takes kb+2
         uint4 wcur[NMAT][4];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wcur[m][q] = wreg[m][q];
+            for (int q = 0; q < 4; ++q) wcur[m][q] = wA[m][q];
         float sc[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) sc[m] = srow[m][kb];
-        if (kb + 1 < nkb) load_kb(kb + 1);  // next block in flight during this one's MFMAs
+        if (kb + 2 < nkb) {
+            load_w(kb + 2, wA);
+            load_a(kb + 2, aA);
+        }
         cz_float16v part[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
@@ -338,7 +389,22 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][i] = __builtin_fmaf(sc[m], part[m][i], acc[m][i]);
-        if (kb + 1 < nkb) stage_a(buf ^ 1);
+        if (kb + 1 < nkb) stage_a(buf ^ 1, aB);  // kb+1's rows (loaded an iteration ago)
+        // rotate: kb+1's weights/rows move to the A set's successor
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 t = wB[m][q];
+                wB[m][q] = wA[m][q];
+                wA[m][q] = t;
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = aB[q];
+            aB[q] = aA[q];
+            aA[q] = t;
+        }
         __syncthreads();
     }
     // epilogue: lane holds rows (i/4)*8 + (l/32)*4 + i%4 of column n

@@ -264,6 +264,97 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
     }
 }
 
+// Many-token router (S > 1): 256 threads = 8 experts x 32 chains, a tile of
+// 16 tokens per workgroup.  Thread (expert e, chain j) keeps one accumulator
+// per token and walks H in chunks of 256 columns: the router elements of its
+// chain come straight from HBM/L2 into registers, the normalised input tile
+// through LDS.  Each chain accumulates in increasing column order, exactly as
+// the one-token kernel, and the same half-wave combine finishes each logit,
+// so logits are bit-identical to the decode router's.  H % 256 == 0.
+#define CZ_RT_TOK 16
+
+__global__ __launch_bounds__(256) void k_router_tiled(StepArgs A) {
+    const LayerDev &L = A.L;
+    const uint32_t H = L.H, E = L.E;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
+    const uint32_t e = blockIdx.x * 8 + wave * 2 + half;
+    const uint32_t ec = min(e, E - 1);
+    const uint32_t t0 = blockIdx.y * CZ_RT_TOK;
+    const uint32_t nt = min((uint32_t)CZ_RT_TOK, (uint32_t)A.S - t0);
+    __shared__ float s_inv[CZ_RT_TOK];
+    __shared__ float s_x[CZ_RT_TOK][256];
+    // 1. per-token 1/rms: wave w handles tokens w, w+4, ... (same order as the
+    //    one-token kernel's lane-strided sum and DPP reduction)
+    for (uint32_t t = wave; t < CZ_RT_TOK; t += 4) {
+        float inv = 1.0f;
+        if (A.rms && t < nt) {
+            // 16 loads in flight per batch, squares summed in column order
+            const float *xs = A.x + (uint64_t)(t0 + t) * H + lane;
+            float ss = 0.0f;
+            for (uint32_t i0 = 0; i0 < H; i0 += 64 * 16) {
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v[q] = i0 + 64 * q < H ? xs[i0 + 64 * q] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    if (i0 + 64 * q < H) {
+                        const float sq = v[q] * v[q];
+                        ss = ss + sq;
+                    }
+                }
+            }
+            ss = cz_wave_sum_dpp(ss);
+            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        }
+        if (lane == 0) s_inv[t] = inv;
+    }
+    __syncthreads();
+    float acc[CZ_RT_TOK];
+#pragma unroll
+    for (int t = 0; t < CZ_RT_TOK; ++t) acc[t] = 0.0f;
+    const float *wr = L.router + (uint64_t)ec * H + j;
+    const bool pub = A.rms && blockIdx.x == 0;
+    // chunk c's router elements and input column, in registers one chunk ahead
+    float w[8], xv[CZ_RT_TOK];
+    auto load_chunk = [&](uint32_t c0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = wr[c0 + 32 * i];
+#pragma unroll
+        for (int t = 0; t < CZ_RT_TOK; ++t)
+            xv[t] = (uint32_t)t < nt ? A.x[(uint64_t)(t0 + t) * H + c0 + tid] : 0.0f;
+    };
+    load_chunk(0);
+    for (uint32_t c0 = 0; c0 < H; c0 += 256) {
+        float wc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wc[i] = w[i];
+        // stage the normalised chunk: thread tid covers column tid of each token
+#pragma unroll
+        for (int t = 0; t < CZ_RT_TOK; ++t) {
+            const float v = A.rms ? xv[t] * s_inv[t] : xv[t];
+            if (pub && (uint32_t)t < nt) {
+                A.xn[(uint64_t)(t0 + t) * H + c0 + tid] = v;
+                if (A.xn_trace) A.xn_trace[(uint64_t)(t0 + t) * H + c0 + tid] = v;
+            }
+            s_x[t][tid] = v;
+        }
+        if (c0 + 256 < H) load_chunk(c0 + 256);  // next chunk in flight during this one's FMAs
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int t = 0; t < CZ_RT_TOK; ++t) acc[t] = __builtin_fmaf(s_x[t][32 * i + j], wc[i], acc[t]);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int t = 0; t < CZ_RT_TOK; ++t) {
+        float lg = cz_router_combine(acc[t], j, hb);
+        if (L.router_bias) lg = lg + L.router_bias[ec];
+        if (j == 0 && e < E && (uint32_t)t < nt) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
+    }
+}
+
 __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
     const uint32_t H = A.L.H, E = A.L.E;
     const uint32_t lane = threadIdx.x & 63;
