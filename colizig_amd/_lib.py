@@ -67,6 +67,12 @@ SIGNATURES = {
     "colizig_hip_expert_read": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp]),
     "colizig_hip_router_read": (ctypes.c_int, [ctypes.c_uint32, vp]),
     "colizig_hip_shared_read": (ctypes.c_int, [ctypes.c_uint32, vp, vp, vp, vp, vp, vp, vp]),
+    "colizig_hip_stream_pool_init": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.c_uint64]),
+    "colizig_hip_layer_stream_from_host": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
+    "colizig_hip_stream_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int, ctypes.c_float]),
+    "colizig_hip_stream_stats": (ctypes.c_int, [c_u64p, ctypes.c_int]),
+    "colizig_hip_host_alloc": (vp, [ctypes.c_uint64]),
+    "colizig_hip_host_free": (None, [vp]),
     "colizig_hip_expf_dev": (ctypes.c_int, [vp, vp, ctypes.c_int]),
     "colizig_hip_expf_host": (ctypes.c_float, [ctypes.c_float]),
     "colizig_hip_malloc": (vp, [ctypes.c_uint64]),

@@ -49,6 +49,14 @@ struct LayerHost {
     float *ss = nullptr;
     float *shg = nullptr;
     float *rbias = nullptr;  // optional router bias [E]
+    // streamed from host memory: experts live in a pinned host slab (same
+    // layout as ew/es) and in slots of the HBM expert pool while cached
+    const uint8_t *host_ew = nullptr;
+    const float *host_es = nullptr;
+    int32_t *slot_map_dev = nullptr;   // [E] device copy of slot_map
+    int32_t *slot_map_stage = nullptr; // [E] pinned staging of the upload
+    std::vector<int32_t> slot_map;     // [E] pool slot or -1
+    std::vector<uint32_t> last_used;   // experts of the previous step (prefetch prediction)
     std::vector<uint8_t> loaded;
     uint32_t nloaded = 0;
     bool shared_set = false;
@@ -57,7 +65,8 @@ struct LayerHost {
     uint64_t es_stride() const { return 3ull * nblk(d.inter) * nblk(d.hidden); }
     uint64_t sw_bytes() const { return 3ull * d.shared_inter * d.hidden; }
     uint64_t ss_floats() const { return 3ull * nblk(d.shared_inter) * nblk(d.hidden); }
-    bool ready() const { return nloaded == d.experts && (d.shared_inter == 0 || shared_set); }
+    bool streamed() const { return host_ew != nullptr; }
+    bool ready() const { return (streamed() || nloaded == d.experts) && (d.shared_inter == 0 || shared_set); }
     LayerDev dev() const {
         LayerDev L{};
         L.H = d.hidden;
@@ -78,6 +87,7 @@ struct LayerHost {
         L.ss = ss;
         L.sh_gate = shg;
         L.router_bias = rbias;
+        L.slot_map = slot_map_dev;
         return L;
     }
 };
@@ -96,6 +106,33 @@ struct Work {
     float *o = nullptr, *os = nullptr;
     size_t cap_counts = 0, cap_offsets = 0, cap_sorted = 0, cap_slot_pos = 0, cap_tok_order = 0, cap_tiles = 0,
            cap_tiles2 = 0, cap_ntiles = 0, cap_o = 0, cap_os = 0;
+};
+
+// ---- HBM expert pool of the streaming tier: fixed-size slots (one expert's
+// gate|up|down weights and scales each), a global LRU over (layer, expert)
+// keys, a side stream for the host->HBM fills.  ExpertCache (moe.zig:121-249)
+// redesigned for one pool shared by every streamed layer.
+struct StreamPool {
+    bool on = false;
+    colizig_dims d{};
+    uint64_t w_slot = 0, s_slot = 0;  // bytes / floats per slot (= ew_stride / es_stride)
+    uint8_t *w = nullptr;
+    float *s = nullptr;
+    uint32_t nslots = 0;
+    std::vector<uint64_t> key;         // 1 + (layer << 32 | expert), 0 = free
+    std::vector<uint64_t> used;        // LRU clock of the last use (or fill)
+    std::vector<uint8_t> prefetched;   // filled by prefetch, not used since
+    std::vector<uint32_t> pin_epoch;   // slot is needed by the layer in flight
+    std::unordered_map<uint64_t, uint32_t> where;
+    uint64_t clock = 0;
+    uint32_t epoch = 0;
+    hipStream_t copy = nullptr;
+    hipEvent_t ev_idx = nullptr, ev_copy = nullptr;
+    uint32_t *h_idx = nullptr;         // pinned routing read-back
+    size_t h_idx_cap = 0;
+    // counters (CacheStats, moe.zig:121-139)
+    uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
+             prefetch_wasted = 0, bytes_h2d = 0;
 };
 
 struct Ctx {
@@ -120,6 +157,7 @@ struct Ctx {
     std::unordered_map<int64_t, hipGraph_t> graph_defs;
     std::unordered_map<int64_t, hipEvent_t> events;
     int64_t next_handle = 1;
+    StreamPool pool;
 };
 
 Ctx g;
@@ -223,9 +261,13 @@ bool grouped_ok(const colizig_dims &d, int S) {
 }
 
 void free_layer(LayerHost &L) {
-    for (void *p : {(void *)L.router, (void *)L.ew, (void *)L.es, (void *)L.sw, (void *)L.ss, (void *)L.shg,
-                    (void *)L.rbias})
+    if (!L.streamed())
+        for (void *p : {(void *)L.ew, (void *)L.es})
+            if (p) (void)hipFree(p);
+    for (void *p : {(void *)L.router, (void *)L.sw, (void *)L.ss, (void *)L.shg, (void *)L.rbias,
+                    (void *)L.slot_map_dev})
         if (p) (void)hipFree(p);
+    if (L.slot_map_stage) (void)hipHostFree(L.slot_map_stage);
     L = LayerHost{};
 }
 
@@ -497,6 +539,12 @@ int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms
     return launch_step(step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace), st);
 }
 
+void pool_drop_layer(uint32_t layer);
+int ensure_h_idx(int S);
+struct LayerHost;
+int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, float *out, int rms, float eps,
+                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st);
+
 LayerHost *find_layer(uint32_t layer) {
     auto it = g.layers.find(layer);
     return it == g.layers.end() ? nullptr : &it->second;
@@ -601,6 +649,14 @@ extern "C" void colizig_cuda_shutdown(void) {
                     (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
+    StreamPool &P = g.pool;
+    if (P.copy) (void)hipStreamSynchronize(P.copy);
+    if (P.w) (void)hipFree(P.w);
+    if (P.s) (void)hipFree(P.s);
+    if (P.h_idx) (void)hipHostFree(P.h_idx);
+    if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
+    if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
+    if (P.copy) (void)hipStreamDestroy(P.copy);
     (void)hipStreamDestroy(g.stream);
     g.~Ctx();
     new (&g) Ctx();
@@ -749,6 +805,8 @@ extern "C" int colizig_hip_layer_init(uint32_t layer, const colizig_dims *dims, 
         return -1;
     }
     (void)hipStreamSynchronize(g.stream);
+    if (g.pool.copy) (void)hipStreamSynchronize(g.pool.copy);
+    pool_drop_layer(layer);
     auto it = g.layers.find(layer);
     if (it != g.layers.end()) free_layer(it->second);
     LayerHost &L = g.layers[layer];
@@ -857,6 +915,15 @@ extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, i
     if (rc) return rc;
     if ((rc = ensure_work(L->d, S))) return rc;
     if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
+    if (L->streamed()) {
+        if ((rc = ensure_work_grouped(L->d, S)) || (rc = ensure_h_idx(S))) return rc ? rc : -2;
+        rc = run_streamed_layer(*L, layer, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, 0, pick_stream(stream));
+        if (rc) return rc;
+        const size_t kb = (size_t)S * L->d.topk * sizeof(float);
+        if (idx_dev) CZ_CHECK(hipMemcpyAsync(idx_dev, g.work.idx, kb, hipMemcpyDeviceToDevice, pick_stream(stream)), -4);
+        if (gates_dev) CZ_CHECK(hipMemcpyAsync(gates_dev, g.work.gates, kb, hipMemcpyDeviceToDevice, pick_stream(stream)), -4);
+        return 0;
+    }
     return launch_layer(*L, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, idx_dev, gates_dev, pick_stream(stream));
 }
 
@@ -875,8 +942,13 @@ extern "C" int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, fl
     if (ensure_host(xb + 2 * kb)) return -2;
     memcpy(g.h_stage, x, xb);
     CZ_CHECK(hipMemcpyAsync(g.work.xin, g.h_stage, xb, hipMemcpyHostToDevice, g.stream), -3);
-    if ((rc = launch_layer(*L, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, nullptr, nullptr, g.stream)))
-        return rc;
+    if (L->streamed()) {
+        if ((rc = ensure_work_grouped(L->d, S)) || (rc = ensure_h_idx(S))) return rc ? rc : -2;
+        rc = run_streamed_layer(*L, layer, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, 0, g.stream);
+    } else {
+        rc = launch_layer(*L, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, nullptr, nullptr, g.stream);
+    }
+    if (rc) return rc;
     char *hs = (char *)g.h_stage;
     CZ_CHECK(hipMemcpyAsync(hs, g.work.out, xb, hipMemcpyDeviceToHost, g.stream), -5);
     CZ_CHECK(hipMemcpyAsync(hs + xb, g.work.idx, kb, hipMemcpyDeviceToHost, g.stream), -5);
@@ -894,6 +966,11 @@ static int chain_enqueue(uint32_t layer0, uint32_t nlayers, float *x_dev, int S,
         LayerHost *L = find_layer(layer0 + l);
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
+        if (L->streamed()) {
+            snprintf(g_err, sizeof g_err, "layer %u streams from host memory: use colizig_hip_stream_decode",
+                     layer0 + l);
+            return -1;
+        }
         if ((rc = ensure_work(L->d, S))) return rc;
         if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
@@ -1025,6 +1102,10 @@ extern "C" int colizig_hip_layer_synth(uint32_t layer, uint64_t seed, float std_
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     LayerHost *L = find_layer(layer);
     if (!g.inited || !L) return -1;
+    if (L->streamed()) {
+        snprintf(g_err, sizeof g_err, "layer %u streams from host memory", layer);
+        return -1;
+    }
     const colizig_dims &d = L->d;
     const uint64_t ls = mix64(seed ^ mix64(0xC011716ull + layer));
     const uint64_t rn = (uint64_t)d.experts * d.hidden;
@@ -1068,6 +1149,10 @@ extern "C" int colizig_hip_expert_read(uint32_t layer, uint32_t expert, unsigned
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     LayerHost *L = find_layer(layer);
     if (!g.inited || !L || expert >= L->d.experts) return -1;
+    if (L->streamed()) {
+        snprintf(g_err, sizeof g_err, "layer %u streams from host memory", layer);
+        return -1;
+    }
     const uint64_t mb = (uint64_t)L->d.inter * L->d.hidden;
     const uint64_t nsc = (uint64_t)nblk(L->d.inter) * nblk(L->d.hidden);
     const uint8_t *wb = L->ew + expert * L->ew_stride();
@@ -1125,6 +1210,7 @@ extern "C" int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers,
         LayerHost *L = find_layer(layer0 + l);
         int rc = check_layer_ready(L, layer0 + l);
         if (rc) return rc;
+        if (L->streamed()) return -1;
         if ((rc = ensure_work(L->d, S))) return rc;
         if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
@@ -1177,10 +1263,312 @@ extern "C" int colizig_hip_expert_slab_read(uint32_t layer, unsigned char *ew, f
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     LayerHost *L = find_layer(layer);
     if (!g.inited || !L || !ew || !es) return -1;
+    if (L->streamed()) {
+        snprintf(g_err, sizeof g_err, "layer %u streams from host memory", layer);
+        return -1;
+    }
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
     CZ_CHECK(hipMemcpy(ew, L->ew, L->ew_stride() * L->d.experts, hipMemcpyDeviceToHost), -5);
     CZ_CHECK(hipMemcpy(es, L->es, L->es_stride() * L->d.experts * sizeof(float), hipMemcpyDeviceToHost), -5);
     return 0;
+}
+
+// ---- streaming tier --------------------------------------------------------------
+namespace {
+
+uint64_t pool_key(uint32_t layer, uint32_t e) { return 1ull + (((uint64_t)layer << 32) | e); }
+
+// A slot for a new entry: a free one, else the least recently used slot not
+// pinned by the layer in flight.  Returns nslots when every slot is pinned.
+uint32_t pool_victim() {
+    StreamPool &P = g.pool;
+    uint32_t best = P.nslots;
+    uint64_t bu = ~0ull;
+    for (uint32_t i = 0; i < P.nslots; ++i) {
+        if (P.key[i] == 0) return i;
+        if (P.pin_epoch[i] == P.epoch) continue;
+        if (P.used[i] < bu) {
+            bu = P.used[i];
+            best = i;
+        }
+    }
+    return best;
+}
+
+// Forgets every pool entry of `layer` (re-registration).
+void pool_drop_layer(uint32_t layer) {
+    StreamPool &P = g.pool;
+    for (uint32_t i = 0; i < P.nslots; ++i)
+        if (P.key[i] && ((P.key[i] - 1) >> 32) == layer) {
+            P.where.erase(P.key[i]);
+            P.key[i] = 0;
+            P.prefetched[i] = 0;
+        }
+}
+
+// Copies expert e of streamed layer L into slot i on the copy stream.
+int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetch) {
+    StreamPool &P = g.pool;
+    if (P.key[i] != 0) {
+        P.where.erase(P.key[i]);
+        P.evictions++;
+        if (P.prefetched[i]) P.prefetch_wasted++;
+    }
+    CZ_CHECK(hipMemcpyAsync(P.w + (uint64_t)i * P.w_slot, L.host_ew + (uint64_t)e * P.w_slot, P.w_slot,
+                            hipMemcpyHostToDevice, P.copy), -3);
+    CZ_CHECK(hipMemcpyAsync(P.s + (uint64_t)i * P.s_slot, L.host_es + (uint64_t)e * P.s_slot,
+                            P.s_slot * sizeof(float), hipMemcpyHostToDevice, P.copy), -3);
+    P.bytes_h2d += P.w_slot + P.s_slot * sizeof(float);
+    P.loads++;
+    P.key[i] = pool_key(layer, e);
+    P.where[P.key[i]] = i;
+    P.used[i] = ++P.clock;
+    P.prefetched[i] = prefetch ? 1 : 0;
+    if (prefetch) P.prefetch_issued++;
+    return 0;
+}
+
+// Makes the experts `sel` of streamed layer `layer` resident (hits touch the
+// LRU, misses are filled on the copy stream), uploads the layer's slot map on
+// the copy stream, and makes the compute stream wait for all of it.
+int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &sel, hipStream_t st) {
+    StreamPool &P = g.pool;
+    P.epoch++;
+    for (uint32_t e : sel) {
+        auto it = P.where.find(pool_key(layer, e));
+        if (it != P.where.end()) {
+            const uint32_t i = it->second;
+            P.hits++;
+            if (P.prefetched[i]) {
+                P.prefetch_hits++;
+                P.prefetched[i] = 0;
+            }
+            P.used[i] = ++P.clock;
+            P.pin_epoch[i] = P.epoch;
+            L.slot_map[e] = (int32_t)i;
+            continue;
+        }
+        P.misses++;
+        const uint32_t i = pool_victim();
+        if (i == P.nslots) {
+            snprintf(g_err, sizeof g_err, "expert pool of %u slots cannot hold one layer's selection", P.nslots);
+            return -2;
+        }
+        int rc = pool_fill(L, layer, e, i, false);
+        if (rc) return rc;
+        P.pin_epoch[i] = P.epoch;
+        P.prefetched[i] = 0;
+        L.slot_map[e] = (int32_t)i;
+    }
+    // the slot map of this layer: only its selected entries matter (others
+    // may be stale and are never read by this layer's kernels)
+    memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
+    CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
+                            hipMemcpyHostToDevice, P.copy), -3);
+    CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
+    CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
+    return 0;
+}
+
+// Prefetch (LastTokenPredictor, predict.zig:29-90): the experts layer `layer`
+// used at the previous step, filled now if absent, behind the fills the
+// compute stream waits for; slots pinned by the layer in flight are spared.
+int stream_prefetch(LayerHost &L, uint32_t layer) {
+    StreamPool &P = g.pool;
+    for (uint32_t e : L.last_used) {
+        if (P.where.count(pool_key(layer, e))) continue;
+        const uint32_t i = pool_victim();
+        if (i == P.nslots) return 0;
+        int rc = pool_fill(L, layer, e, i, true);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int ensure_h_idx(int S) {
+    StreamPool &P = g.pool;
+    const size_t kmax = (size_t)S * CZ_MAX_K;
+    if (P.h_idx_cap >= kmax) return 0;
+    if (P.h_idx) (void)hipHostFree(P.h_idx);
+    P.h_idx = nullptr;
+    P.h_idx_cap = 0;
+    if (hipHostMalloc(&P.h_idx, kmax * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) return -2;
+    P.h_idx_cap = kmax;
+    return 0;
+}
+
+// One streamed layer: router and routing on the compute stream, the routing
+// read back; once it is on the host (every earlier kernel has then finished)
+// hits, fills of the misses and the slot map; then the next streamed layer's
+// predicted experts start filling behind them, sparing the slots this layer's
+// kernels will read; then the layer's expert kernels, after its fills.
+// Scratch (ensure_work + ensure_work_grouped) and h_idx must be in place.
+int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, float *out, int rms, float eps,
+                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st) {
+    StreamPool &P = g.pool;
+    Work &w = g.work;
+    const StepArgs A = step_args(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr);
+    launch_router(A, st);
+    GroupArgs G{};
+    G.L = A.L;
+    G.S = S;
+    G.xn = rms ? w.xn : x;
+    G.logits = w.logits;
+    G.idx = w.idx;
+    G.gates = w.gates;
+    G.sgate = w.sgate;
+    G.tok_order = w.tok_order;
+    switch (cz_route_groups(A.L.E)) {
+        case 1: launch_route_tokens<1>(G, st); break;
+        case 2: launch_route_tokens<2>(G, st); break;
+        case 4: launch_route_tokens<4>(G, st); break;
+        case 8: launch_route_tokens<8>(G, st); break;
+        default: launch_route_tokens<16>(G, st); break;
+    }
+    const size_t nk = (size_t)S * L.d.topk;
+    CZ_CHECK(hipMemcpyAsync(P.h_idx, w.idx, nk * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
+    CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
+    // the routing is on the critical path: poll for it rather than block
+    for (;;) {
+        const hipError_t q = hipEventQuery(P.ev_idx);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) {
+            snprintf(g_err, sizeof g_err, "routing read-back: %s", hipGetErrorString(q));
+            return -5;
+        }
+    }
+    std::vector<uint32_t> sel;
+    for (size_t k = 0; k < nk; ++k) {
+        const uint32_t e = std::min(P.h_idx[k], L.d.experts - 1);
+        if (std::find(sel.begin(), sel.end(), e) == sel.end()) sel.push_back(e);
+    }
+    int rc = stream_resident(L, layer, sel, st);
+    if (rc) return rc;
+    L.last_used = sel;
+    if (next && next->streamed() && (rc = stream_prefetch(*next, next_layer))) return rc;
+    if (grouped_ok(L.d, S)) return launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st);
+    return launch_step(A, st, kUp | kDown);
+}
+
+}  // namespace
+
+extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t cap_bytes) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !dims) return -1;
+    StreamPool &P = g.pool;
+    if (P.on) {
+        snprintf(g_err, sizeof g_err, "expert pool already configured");
+        return -1;
+    }
+    const colizig_dims d = *dims;
+    const uint64_t w_slot = 3ull * d.inter * d.hidden, s_slot = 3ull * nblk(d.inter) * nblk(d.hidden);
+    const uint64_t per = w_slot + s_slot * sizeof(float);
+    const uint32_t n = (uint32_t)std::min<uint64_t>(cap_bytes / per, 1u << 24);
+    if (n < d.topk) {
+        snprintf(g_err, sizeof g_err, "pool of %llu bytes holds %u experts < top-k %u", (unsigned long long)cap_bytes,
+                 n, d.topk);
+        return -1;
+    }
+    if (hipMalloc(&P.w, w_slot * n) != hipSuccess || hipMalloc(&P.s, s_slot * n * sizeof(float)) != hipSuccess) {
+        if (P.w) (void)hipFree(P.w);
+        P.w = nullptr;
+        snprintf(g_err, sizeof g_err, "expert pool allocation of %u slots failed", n);
+        return -2;
+    }
+    CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);
+    CZ_CHECK(hipEventCreateWithFlags(&P.ev_idx, hipEventDisableTiming), -4);
+    CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy, hipEventDisableTiming), -4);
+    P.d = d;
+    P.w_slot = w_slot;
+    P.s_slot = s_slot;
+    P.nslots = n;
+    P.key.assign(n, 0);
+    P.used.assign(n, 0);
+    P.prefetched.assign(n, 0);
+    P.pin_epoch.assign(n, 0);
+    P.on = true;
+    return 0;
+}
+
+extern "C" int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host_ew,
+                                                  const float *host_es) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    StreamPool &P = g.pool;
+    if (!g.inited || !L || !host_ew || !host_es || !P.on) return -1;
+    const colizig_dims &d = L->d;
+    if (d.hidden != P.d.hidden || d.inter != P.d.inter) {
+        snprintf(g_err, sizeof g_err, "layer %u shape differs from the expert pool's", layer);
+        return -1;
+    }
+    (void)hipStreamSynchronize(g.stream);
+    if (!L->streamed()) {
+        if (L->ew) (void)hipFree(L->ew);
+        if (L->es) (void)hipFree(L->es);
+    }
+    L->host_ew = host_ew;
+    L->host_es = host_es;
+    L->ew = P.w;
+    L->es = P.s;
+    L->slot_map.assign(d.experts, -1);
+    if (!L->slot_map_dev && hipMalloc(&L->slot_map_dev, d.experts * sizeof(int32_t)) != hipSuccess) return -2;
+    CZ_CHECK(hipMemset(L->slot_map_dev, 0xff, d.experts * sizeof(int32_t)), -4);  // all -1
+    if (!L->slot_map_stage && hipHostMalloc(&L->slot_map_stage, d.experts * sizeof(int32_t), hipHostMallocDefault) !=
+                                  hipSuccess)
+        return -2;
+    L->last_used.clear();
+    pool_drop_layer(layer);
+    return 0;
+}
+
+extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    StreamPool &P = g.pool;
+    if (!g.inited || !P.on || S < 1 || !x_dev || nlayers == 0) return -1;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        int rc = check_layer_ready(L, layer0 + l);
+        if (rc) return rc;
+        if ((rc = ensure_work(L->d, S))) return rc;
+        if ((rc = ensure_work_grouped(L->d, S))) return rc;
+    }
+    if (ensure_h_idx(S)) return -2;
+    hipStream_t st = g.stream;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost &L = *find_layer(layer0 + l);
+        LayerHost *next = l + 1 < nlayers ? find_layer(layer0 + l + 1) : nullptr;
+        const int rc = L.streamed()
+                           ? run_streamed_layer(L, layer0 + l, x_dev, S, x_dev, 1, eps, x_dev, next, layer0 + l + 1, st)
+                           : launch_layer(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, st);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+extern "C" int colizig_hip_stream_stats(uint64_t *out, int n) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const StreamPool &P = g.pool;
+    const uint64_t v[10] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
+                            P.prefetch_wasted, P.bytes_h2d, P.nslots, (uint64_t)P.where.size()};
+    if (!out || n < 1) return -1;
+    for (int i = 0; i < n && i < 10; ++i) out[i] = v[i];
+    return 0;
+}
+
+extern "C" void *colizig_hip_host_alloc(uint64_t bytes) {
+    CsrGuard csr;
+    void *p = nullptr;
+    if (!g.inited || bytes == 0 || hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) return nullptr;
+    return p;
+}
+
+extern "C" void colizig_hip_host_free(void *p) {
+    CsrGuard csr;
+    if (g.inited && p) (void)hipHostFree(p);
 }
 
 // ---- exp test hooks -------------------------------------------------------------

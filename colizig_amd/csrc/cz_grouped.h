@@ -282,8 +282,9 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
     }
     __syncthreads();
 
-    const uint8_t *W0 = P.w0 + (uint64_t)e * P.w_stride;
-    const float *S0 = P.s0 + (uint64_t)e * P.s_stride;
+    const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
+    const uint8_t *W0 = P.w0 + sl * P.w_stride;
+    const float *S0 = P.s0 + sl * P.s_stride;
     // this wave's 32 output columns, this lane's weight row n and K half
     const uint32_t n_base = nt * CZ_GG_N + wave * 32;
     const uint32_t n = n_base + (lane & 31);

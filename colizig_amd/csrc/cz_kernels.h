@@ -36,7 +36,17 @@ struct LayerDev {
     const float *ss;       // shared scales (gate|up|down)
     const float *sh_gate;  // [H]
     const float *router_bias;  // [E] added to each logit, or null (workload shaping only)
+    const int32_t *slot_map;   // [E] HBM pool slot of each expert (layers streamed from
+                               // host memory; ew/es then point at the pool), or null
 };
+
+// Slot of expert e in ew/es: e itself for a resident layer, the pool slot for
+// a streamed one (the host makes every selected expert resident before the
+// layer's expert kernels run; a negative entry maps to slot 0 so that a read
+// stays in bounds).
+__device__ inline uint64_t cz_slot(const LayerDev &L, uint32_t e) {
+    return L.slot_map ? (uint64_t)max(L.slot_map[e], 0) : (uint64_t)e;
+}
 
 #define CZ_ROUTER_TT 4    // most tokens per router tile
 #define CZ_MAX_E 1024     // experts supported by the top-k wave
@@ -502,10 +512,11 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
             }
         }
         const uint32_t e = s_idx[z];
-        const uint8_t *base = L.ew + (uint64_t)e * L.ew_stride;
+        const uint64_t sl = cz_slot(L, e);
+        const uint8_t *base = L.ew + sl * L.ew_stride;
         it.Wg = base;
         it.Wu = base + (uint64_t)L.I * L.H;
-        const float *sb = L.es + (uint64_t)e * L.es_stride;
+        const float *sb = L.es + sl * L.es_stride;
         it.Sg = sb;
         it.Su = sb + (uint64_t)L.nbI * L.nbH;
         it.out = A.h + (uint64_t)slot * L.I;
@@ -692,9 +703,10 @@ __device__ inline void cz_down_row(const StepArgs &A, uint32_t tok, uint32_t r, 
         for (int c = 0; c < KC; ++c) {
             const uint32_t z = min(z0 + c, L.K - 1);
             const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_e, z), L.E - 1);
-            const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
+            const uint64_t sl = cz_slot(L, e);
+            const uint8_t *Wd = L.ew + sl * L.ew_stride + 2ull * L.I * L.H;
             cz_load_row<NBI>(Wd + (uint64_t)r * L.I + col0, dd[c]);
-            cz_load_scales<NBI>(L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI,
+            cz_load_scales<NBI>(L.es + sl * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI,
                                 col0, sd[c]);
         }
 #pragma unroll
@@ -784,8 +796,9 @@ __global__ __launch_bounds__(256) void k_down_generic(StepArgs A) {
     for (uint32_t z = 0; z < L.K; ++z) {
         const uint32_t slot = tok * L.K + z;
         const uint32_t e = A.idx[slot];
-        const uint8_t *Wd = L.ew + (uint64_t)e * L.ew_stride + 2ull * L.I * L.H;
-        const float *Sd = L.es + (uint64_t)e * L.es_stride + 2ull * L.nbI * L.nbH;
+        const uint64_t sl = cz_slot(L, e);
+        const uint8_t *Wd = L.ew + sl * L.ew_stride + 2ull * L.I * L.H;
+        const float *Sd = L.es + sl * L.es_stride + 2ull * L.nbI * L.nbH;
         const float p = cz_dot_fp8_strided(Wd + (uint64_t)r * L.I, Sd + (uint64_t)(r / CZ_BLOCK) * L.nbI,
                                            A.h + (uint64_t)slot * L.I, L.I, lane);
         acc = __builtin_fmaf(A.gates[slot], p, acc);

@@ -237,3 +237,57 @@ class DeviceBuffer:
         if self.ptr:
             _lib.hip().colizig_hip_free(self.ptr)
             self.ptr = None
+
+
+class HostBuffer:
+    """Pinned host memory through the library, viewed as a numpy array."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = nbytes
+        self.ptr = _lib.hip().colizig_hip_host_alloc(nbytes)
+        if not self.ptr:
+            raise GpuBackendError("colizig_hip_host_alloc", -2)
+        self.array = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(self.ptr))
+
+    def view(self, dtype) -> np.ndarray:
+        return self.array.view(dtype)
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.hip().colizig_hip_host_free(self.ptr)
+            self.ptr = None
+
+
+STREAM_STAT_NAMES = ("hits", "misses", "loads", "evictions", "prefetch_issued", "prefetch_hits",
+                     "prefetch_wasted", "bytes_h2d", "slots", "resident")
+
+
+def stream_pool_init(d: Dims, cap_bytes: int) -> None:
+    _check("colizig_hip_stream_pool_init", _lib.hip().colizig_hip_stream_pool_init(ctypes.byref(d), cap_bytes))
+
+
+def stream_stats() -> dict:
+    v = (ctypes.c_uint64 * len(STREAM_STAT_NAMES))()
+    _check("colizig_hip_stream_stats", _lib.hip().colizig_hip_stream_stats(v, len(STREAM_STAT_NAMES)))
+    return dict(zip(STREAM_STAT_NAMES, (int(x) for x in v)))
+
+
+def host_expert_slab(d: Dims, experts: list) -> tuple[HostBuffer, HostBuffer]:
+    """Pinned host slabs of a layer's experts in the HBM slab layout
+    (expert e: gate | up | down bytes; its scales likewise)."""
+    H, I, E = d.hidden, d.inter, d.experts
+    mat, nsc = I * H, nblk(I) * nblk(H)
+    wb = HostBuffer(E * 3 * mat)
+    sb = HostBuffer(E * 3 * nsc * 4)
+    w = wb.view(np.uint8).reshape(E, 3, mat)
+    sc = sb.view(np.float32).reshape(E, 3, nsc)
+    for e, ex in enumerate(experts):
+        for r, k in enumerate(("gate", "up", "down")):
+            w[e, r] = np.ascontiguousarray(ex[k + "_w"], np.uint8).ravel()
+            sc[e, r] = np.ascontiguousarray(ex[k + "_s"], np.float32).ravel()
+    return wb, sb
+
+
+def stream_layer_from_host(layer: int, wb: HostBuffer, sb: HostBuffer) -> None:
+    _check("colizig_hip_layer_stream_from_host",
+           _lib.hip().colizig_hip_layer_stream_from_host(layer, wb.ptr, sb.ptr))

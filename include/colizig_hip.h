@@ -157,6 +157,44 @@ void colizig_hip_graph_destroy(int64_t handle);
 int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, int reps,
                                    float *us_out);
 
+/* ---- streaming tier: experts in pinned host memory, cached in HBM -------
+ * ExpertCache (moe.zig:121-249) + loadExpert redesigned for one GPU: one HBM
+ * pool of fixed-size expert slots shared by every streamed layer, a global
+ * LRU over (layer, expert), fills by hipMemcpyAsync from pinned host memory
+ * on a side stream that the compute stream waits for, and a last-step
+ * predictor (predict.zig:29-90) that starts filling the next layer's likely
+ * experts while the current layer computes. */
+
+/* Creates the pool: floor(cap_bytes / slot) slots for experts of shape
+ * (dims->hidden, dims->inter), slot = 3*I*H bytes + 3*nblk(I)*nblk(H) floats.
+ * Once per context.  -1 when the pool would hold fewer than top-k experts. */
+int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t cap_bytes);
+
+/* Makes a registered layer stream its experts from host memory: host_ew /
+ * host_es hold all E experts in the HBM slab layout (expert e at e*3*I*H
+ * bytes: gate | up | down; scales at e*3*nblk(I)*nblk(H) floats), pinned
+ * (colizig_hip_host_alloc), caller-owned, valid until the layer is
+ * re-registered or the context shut down.  The layer's own HBM expert slab
+ * is released. */
+int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host_ew, const float *host_es);
+
+/* colizig_hip_chain_decode over layers some of which stream: per streamed
+ * layer the routing is read back to the host, misses are filled, the next
+ * streamed layer's predicted experts are prefetched, then the expert kernels
+ * run.  Returns after the last layer is enqueued (the host waits once per
+ * streamed layer for its routing).  colizig_hip_moe_forward and
+ * colizig_hip_moe_forward_dev accept streamed layers the same way; the
+ * plain chain, its graph and the read-back hooks refuse them (-1). */
+int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps);
+
+/* Pool counters, out[0..n): hits, misses, loads, evictions, prefetch_issued,
+ * prefetch_hits, prefetch_wasted, bytes_h2d, slots, resident entries. */
+int colizig_hip_stream_stats(uint64_t *out, int n);
+
+/* Pinned host memory for the host expert slabs. */
+void *colizig_hip_host_alloc(uint64_t bytes);
+void colizig_hip_host_free(void *p);
+
 /* Fills a registered layer (router, every expert, shared expert) with
  * seeded synthetic weights directly in HBM: router and sh_gate f32
  * N(0, std_router); expert matrices N(0, std_w) quantised per 128x128 block

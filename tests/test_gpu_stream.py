@@ -1,0 +1,103 @@
+"""Streaming tier: experts in pinned host memory, an HBM pool smaller than
+the working set.  A streamed layer runs the same kernels on the same bytes
+as a resident one, so outputs are bit-identical; the pool counters follow
+the cache's invariants (moe.zig:711-741: hits + misses = uses, every miss
+and prefetch is one load)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from colizig_amd import _lib, moe, synth
+from tests.helpers import f32_bits
+
+pytestmark = pytest.mark.gpu
+
+H, E, K, I = 512, 16, 4, 256
+D = moe.dims(H, E, K, I)
+SLOT = 3 * I * H + 3 * moe.nblk(I) * moe.nblk(H) * 4
+_state = {}
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+NSLOTS = 16  # = E: one layer's whole selection fits at any S; 4 layers x 16 experts do not
+
+
+@pytest.fixture(scope="module")
+def pool(gpu):
+    """One pool per context."""
+    moe.stream_pool_init(D, NSLOTS * SLOT)
+    return True
+
+
+def _layers(base_res, base_str, nl, seed, zipf=True):
+    hosts, keep = [], []
+    for l in range(nl):
+        h = synth.make_layer(H, E, K, I, 0, True, seed=seed + l)
+        if zipf:
+            h["router_bias"] = synth.zipf_router_bias(E, 1.2, seed=seed + l)
+        hosts.append(h)
+        moe.register_layer(base_res + l, h)
+        moe.register_layer(base_str + l, h)
+        wb, sb = moe.host_expert_slab(D, h["experts"])
+        moe.stream_layer_from_host(base_str + l, wb, sb)
+        keep += [wb, sb]
+    _state.setdefault("keep", []).extend(keep)  # pinned slabs live as long as the layers
+    return hosts
+
+
+def test_stream_chain_bit_identical_to_resident(pool):
+    say("stream chain vs resident, 4 layers, 16-slot pool")
+    nl = 4
+    _layers(2000, 2100, nl, seed=31)
+    hip = _lib.hip()
+    x0 = synth.hidden_states(1, H, seed=31)
+    xr, xs = moe.DeviceBuffer(x0.nbytes), moe.DeviceBuffer(x0.nbytes)
+    xr.upload(x0)
+    xs.upload(x0)
+    st0 = moe.stream_stats()
+    steps = 8
+    for t in range(steps):
+        assert hip.colizig_hip_chain_decode(2000, nl, xr.ptr, 1, 1e-6, None, None, None, None) == 0
+        assert hip.colizig_hip_stream_decode(2100, nl, xs.ptr, 1, 1e-6) == 0, _lib.last_error()
+        assert hip.colizig_hip_sync() == 0
+        a = xr.download(np.empty_like(x0))
+        b = xs.download(np.empty_like(x0))
+        assert np.array_equal(f32_bits(a), f32_bits(b)), f"step {t}"
+    st = {k: v - st0[k] for k, v in moe.stream_stats().items() if k not in ("slots", "resident")}
+    say(f"  {st}")
+    uses = steps * nl * K  # S=1: K distinct experts per layer per step
+    assert st["hits"] + st["misses"] == uses
+    assert st["loads"] == st["misses"] + st["prefetch_issued"]
+    assert st["bytes_h2d"] == st["loads"] * SLOT
+    assert st["misses"] > 0
+    if st["loads"] > NSLOTS:
+        assert st["evictions"] > 0
+
+
+def test_stream_moe_forward_bit_identical(pool):
+    say("stream moe_forward vs resident, S=1 and S=32")
+    _layers(2200, 2300, 1, seed=41)
+    Lr = moe.Layer(2200, D, True)
+    Ls = moe.Layer(2300, D, True)
+    for S in (1, 3, 32):  # S = 32 takes the grouped regime
+        x = synth.hidden_states(S, H, seed=41 + S)
+        a, ia, ga = Lr.forward(x)
+        b, ib, gb = Ls.forward(x)
+        assert np.array_equal(ia, ib) and np.array_equal(f32_bits(ga), f32_bits(gb))
+        assert np.array_equal(f32_bits(a), f32_bits(b)), f"S={S}"
+
+
+def test_stream_refused_by_plain_chain(pool):
+    _layers(2400, 2500, 1, seed=51, zipf=False)
+    hip = _lib.hip()
+    xb = moe.DeviceBuffer(H * 4)
+    xb.upload(np.zeros((1, H), np.float32))
+    assert hip.colizig_hip_chain_decode(2500, 1, xb.ptr, 1, 1e-6, None, None, None, None) == -1
+    assert hip.colizig_hip_chain_graph_create(2500, 1, xb.ptr, 1, 1e-6) < 0
