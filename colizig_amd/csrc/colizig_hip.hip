@@ -279,7 +279,7 @@ int router_tokens_per_tile(uint32_t H) {
     return (int)std::min<uint32_t>(CZ_ROUTER_TT, std::max<uint32_t>(1u, 8192u / std::max<uint32_t>(H, 1u)));
 }
 
-constexpr int kUpRows = 2;    // rows of each of gate/up per wave
+constexpr int kUpRows = 1;    // rows of each of gate/up per wave
 constexpr int kDownKC = 8;    // experts per load batch of the down kernel
 
 enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };

@@ -75,21 +75,28 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     const uint32_t lane = cz_lane(), wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * 4 + wave;
     if (t >= (uint32_t)G.S) return;  // wave-uniform
-    cz_route_wave_m<M>(G.logits + (uint64_t)t * L.E, L.E, L.K, L.norm_topk, s_idx[wave], s_gate[wave]);
-    uint32_t my_e = 0xffffffffu;
-    if (lane < L.K) {  // lane z reads back the entry it wrote
-        const uint64_t o = (uint64_t)t * L.K + lane;
-        my_e = s_idx[wave][lane];
-        G.idx[o] = my_e;
-        G.gates[o] = s_gate[wave][lane];
-        if (G.idx_trace) G.idx_trace[o] = my_e;
-        if (G.gates_trace) G.gates_trace[o] = s_gate[wave][lane];
+    uint32_t o_pos = 0, o_id = 0;
+    float o_gate = 0.0f;
+    cz_route_wave_m<M>(G.logits + (uint64_t)t * L.E, L.E, L.K, L.norm_topk, s_idx[wave], s_gate[wave], o_pos, o_id,
+                       o_gate);
+    const uint32_t my_e = lane < L.K ? o_id : 0xffffffffu;
+    if (lane < L.K) {  // lane z holds one pick; o_pos is its place in pick order
+        const uint64_t o = (uint64_t)t * L.K + o_pos;
+        G.idx[o] = o_id;
+        G.gates[o] = o_gate;
+        if (G.idx_trace) G.idx_trace[o] = o_id;
+        if (G.gates_trace) G.gates_trace[o] = o_gate;
     }
-    // the token's slots in ascending expert id (the K ids are distinct): lane
-    // z's rank is the number of the token's experts below its own
+    // the token's slots in ascending expert id: a pick's rank is the number
+    // of the token's picks with a lower id (equal ids, possible only when NaN
+    // logits leave fewer than K candidates, are ordered by lane); its slot is
+    // t*K + its place in pick order
     uint32_t rank = 0;
-    for (uint32_t q = 0; q < L.K; ++q) rank += (uint32_t)__builtin_amdgcn_readlane((int)my_e, q) < my_e ? 1u : 0u;
-    if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + lane;
+    for (uint32_t q = 0; q < L.K; ++q) {
+        const uint32_t eq = (uint32_t)__builtin_amdgcn_readlane((int)my_e, q);
+        rank += (eq < my_e || (eq == my_e && q < lane)) ? 1u : 0u;
+    }
+    if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + o_pos;
     if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         const float *xs = G.xn + (uint64_t)t * L.H;
         float d = 0.0f;

@@ -391,12 +391,14 @@ __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
 // picked v in f64 in pick order; den = norm_topk ? top : sum_e f64(v_e) in
 // expert order; gate_z = f32(f64(v_z) / den).  Lane l holds experts
 // l + 64m for m < M (M = ceil(E/64)); values move between lanes by DPP,
-// readlane and ballot only.  Lanes z < K write s_idx[z] / s_gate[z] (LDS),
-// which the block reads after a barrier.  Must be called by a whole wave.
+// readlane and ballot only.  Lane z < K leaves pick z in registers (o_pos =
+// z, o_id, o_gate) and writes s_idx[z] / s_gate[z] (LDS), which the block
+// reads after a barrier.  Must be called by a whole wave.
 // ---------------------------------------------------------------------------
 template <int M>
 __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
-                                       uint32_t *s_idx, float *s_gate) {
+                                       uint32_t *s_idx, float *s_gate, uint32_t &o_pos, uint32_t &o_id,
+                                       float &o_gate) {
     const uint32_t lane = cz_lane();
     float v[M];
 #pragma unroll
@@ -453,8 +455,11 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
     }
     if (lane < K) {
         const double den = norm_topk ? top : all;  // moe.zig:461-462
-        s_idx[lane] = my_i;
-        s_gate[lane] = (float)((double)my_v / den);
+        o_pos = lane;
+        o_id = my_i;
+        o_gate = (float)((double)my_v / den);
+        s_idx[lane] = o_id;
+        s_gate[lane] = o_gate;
     }
 }
 
@@ -487,11 +492,20 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
     uint32_t blk = blockIdx.x;
     UpItem it;
     // the block's token row of the router input, staged in LDS while the
-    // routing runs (H/4 float4, H a multiple of 4)
-    auto stage_x = [&](uint32_t tok) {
-        if (xs_lds) {
-            const float4 *src = (const float4 *)(xn + (uint64_t)tok * L.H);
-            for (uint32_t i = threadIdx.x; i < L.H / 4; i += blockDim.x) xs_lds[i] = src[i];
+    // routing runs (H/4 float4, H a multiple of 4): threads [first,
+    // blockDim) issue two loads at a time before storing them
+    auto stage_x = [&](uint32_t tok, uint32_t first) {
+        if (!xs_lds || threadIdx.x < first) return;
+        const float4 *src = (const float4 *)(xn + (uint64_t)tok * L.H);
+        const uint32_t n4 = L.H / 4, step = blockDim.x - first;
+        for (uint32_t i0 = threadIdx.x - first; i0 < n4; i0 += 2 * step) {
+            float4 r[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (i0 + q * step < n4) r[q] = src[i0 + q * step];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (i0 + q * step < n4) xs_lds[i0 + q * step] = r[q];
         }
     };
     if (blk < nslots * tiles_r) {
@@ -499,8 +513,13 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         it.tile = blk - slot * tiles_r;
         it.tok = slot / L.K;
         const uint32_t z = slot - it.tok * L.K;
-        stage_x(it.tok);
-        if (wave == 0) cz_route_wave_m<M>(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate);
+        stage_x(it.tok, 0);
+        if (wave == 0) {
+            uint32_t o_pos = 0, o_id = 0;
+            float o_gate = 0.0f;
+            cz_route_wave_m<M>(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate, o_pos, o_id,
+                               o_gate);
+        }
         __syncthreads();
         if (z == 0 && it.tile == 0 && wave == 0) {
             for (uint32_t k = lane; k < L.K; k += 64) {
@@ -534,7 +553,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         it.out = A.hs + (uint64_t)it.tok * L.SI;
         it.rows = L.SI;
         it.routed = false;
-        stage_x(it.tok);
+        stage_x(it.tok, 0);
         // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         if (it.tile == 0 && wave == 0) {
             const float *xs = xn + (uint64_t)it.tok * L.H;

@@ -308,3 +308,24 @@ def test_qwen3_30b_shape_two_layers(gpu, oracle_lib):
             out_g = layers[l].forward(xn[l])[0]
             out_o = orcs[l].forward(xn[l])[0]
             assert rel_l2(out_g, out_o) < RTOL_L2
+
+
+@pytest.mark.parametrize("S", [1, 20])
+def test_routing_exact_ties_pick_lowest_id(gpu, oracle_lib, S):
+    """Router rows duplicated so several experts get bit-identical logits:
+    the scan's strict '>' keeps the lowest id first (moe.zig:447-460), in the
+    decode (S=1) and grouped (S=20) regimes."""
+    say(f"exact ties S={S}")
+    host = synth.make_layer(512, 64, 8, 256, 0, True, seed=123)
+    r = host["router"]
+    for a, b in [(3, 40), (7, 8), (8, 63), (20, 21), (21, 22)]:
+        r[b] = r[a]
+    host["router"] = r
+    Lg = moe.register_layer(650 + S, host)
+    Lo = oracle_lib.OracleLayer(host)
+    x = synth.hidden_states(S, 512, seed=5)
+    _check_forward(Lg, Lo, x, f"ties S={S}")
+    # the tie groups really occur in the selected sets
+    _, idx, _ = Lo.forward(x)
+    assert any(len({3, 40} & set(row)) == 2 or len({7, 8, 63} & set(row)) >= 2 or len({20, 21, 22} & set(row)) >= 2
+               for row in idx.tolist()) or S == 1
