@@ -73,10 +73,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
-    ap.add_argument("--workload", choices=["decode", "prefill", "stream"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4"], default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
                          "512 tokens with Zipf(1.1) routing skew (grouped regime); stream: batch-1 decode "
-                         "with the expert set in pinned host memory and a 16 GB HBM expert pool")
+                         "with the expert set in pinned host memory and a 16 GB HBM expert pool; qwen4: "
+                         "Qwen4-Exp-style stack (36 layers, H4096, E512 top-10, shared 4096) at batch 1 and 32")
     ap.add_argument("--pool-gb", type=float, default=16.0, help="stream: HBM expert pool cap (GB)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -94,6 +95,9 @@ def main():
         return
     if args.workload == "stream":
         stream_bench(args)
+        return
+    if args.workload == "qwen4":
+        qwen4_bench(args)
         return
 
     from colizig_amd import _lib, moe
@@ -376,6 +380,75 @@ def stream_bench(args) -> None:
     print(json.dumps(line), flush=True)
     for wb, sb in host:
         pass  # pinned slabs stay alive until the process ends (the layers point at them)
+
+
+def qwen4_bench(args) -> None:
+    """Qwen4-Exp-style MoE stack (synthetic shapes): 36 layers, hidden 4096,
+    512 routed experts top-10 + 1 always-on shared expert, moe_intermediate
+    512, shared_intermediate 4096, block-FP8 weights (116 GB resident).
+    Decode at batch 1 (decode kernels) and at batch 32 independent rows
+    (grouped regime), each a HIP graph of the chained step."""
+    from colizig_amd import _lib, moe
+    H, E, K, I, SI, NL = 4096, 512, 10, 512, 4096, 36
+    c = dict(workload="qwen4-exp-moe-decode", layers=NL, hidden=H, experts=E, topk=K, inter=I, shared_inter=SI,
+             norm_topk=1, weights="block-fp8-e4m3-128x128", seed=0)
+    name = moe.init()
+    log(f"device: {name}")
+    hip = _lib.hip()
+    d = moe.dims(H, E, K, I, SI, True)
+    zero_router = np.zeros((E, H), np.float32)
+    t0 = time.time()
+    for l in range(NL):
+        moe.Layer.load(l, d, zero_router).synth(seed=7 * l + 3)
+    log(f"weights generated in HBM: {NL} layers in {time.time() - t0:.1f}s")
+    per_expert = 3 * H * I + 4 * 3 * nblk(I) * nblk(H)
+    shared = 3 * H * SI + 4 * 3 * nblk(SI) * nblk(H) + H * 4
+    router = E * H * 4
+    out = {}
+    for S in (1, 32):
+        x0 = np.random.default_rng(S).normal(0.0, 1.0, size=(S, H)).astype(np.float32)
+        xb = moe.DeviceBuffer(x0.nbytes)
+        idx_t = moe.DeviceBuffer(NL * S * K * 4)
+        xb.upload(x0)
+        assert hip.colizig_hip_chain_decode(0, NL, xb.ptr, S, 1e-6, None, idx_t.ptr, None, None) == 0
+        assert hip.colizig_hip_sync() == 0
+        idx = idx_t.download(np.empty((NL, S, K), np.uint32))
+        touched = sum(int(np.unique(idx[l]).size) for l in range(NL))
+        step_bytes = touched * per_expert + NL * (shared + router + 2 * S * H * 4)
+        xb.upload(x0)
+        gh = hip.colizig_hip_chain_graph_create(0, NL, xb.ptr, S, 1e-6)
+        assert gh > 0, _lib.last_error()
+        for _ in range(args.warmup):
+            assert hip.colizig_hip_graph_launch(gh, None) == 0
+        assert hip.colizig_hip_sync() == 0
+        ev0, ev1 = hip.colizig_hip_event_create(), hip.colizig_hip_event_create()
+        steps = max(8, args.steps // (4 if S > 1 else 1))
+        hip.colizig_hip_event_record(ev0, None)
+        for _ in range(steps):
+            hip.colizig_hip_graph_launch(gh, None)
+        hip.colizig_hip_event_record(ev1, None)
+        assert hip.colizig_hip_sync() == 0
+        ms = hip.colizig_hip_event_elapsed_ms(ev0, ev1) / steps
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        out[S] = dict(tok_s=round(S * 1000.0 / ms, 1), ms_per_step=round(ms, 4), hbm_gbs=round(gbs, 1),
+                      hbm_frac=round(gbs / HBM_PEAK_GBS, 4), experts_touched_per_layer=round(touched / NL, 1),
+                      bytes_per_step=step_bytes)
+        log(f"qwen4 S={S}: {ms:.3f} ms/step, {S * 1000.0 / ms:.1f} tok/s, {gbs:.0f} GB/s "
+            f"({touched / NL:.1f} experts/layer)")
+        hip.colizig_hip_graph_destroy(gh)
+        xb.free()
+        idx_t.free()
+    line = {
+        "metric": "MoE decode tok/s, Qwen4-Exp-style stack (36 L, E512 top-10 + shared), 1 MI355X",
+        "value": out[1]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": out[1]["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "e4m3-weights/f32-accumulate", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) hidden states)",
+        "config": {**c, "parallelism": "none (1 GPU)", "global_batch": 1, "seq_len": 1},
+        "batch1": out[1], "batch32": out[32],
+        "roofline": {"bound": "hbm", "achieved": out[1]["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": out[1]["hbm_frac"], "traffic": None, "scope": "whole step, batch 1"},
+    }
+    print(json.dumps(line), flush=True)
 
 
 def calibrate_copy(mib: int) -> None:

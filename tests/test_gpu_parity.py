@@ -329,3 +329,20 @@ def test_routing_exact_ties_pick_lowest_id(gpu, oracle_lib, S):
     _, idx, _ = Lo.forward(x)
     assert any(len({3, 40} & set(row)) == 2 or len({7, 8, 63} & set(row)) >= 2 or len({20, 21, 22} & set(row)) >= 2
                for row in idx.tolist()) or S == 1
+
+
+@pytest.mark.parametrize("S", [1, 32])
+def test_qwen4_exp_shape_layer(gpu, oracle_lib, S):
+    """Qwen4-Exp-style layer at full size: hidden 4096, 512 experts, top-10,
+    moe_intermediate 512, one sigmoid-gated shared expert of 4096 (FP8), at
+    batch 1 (decode kernels) and batch 32 (grouped regime); GPU-generated
+    weights read back for the oracle."""
+    say(f"qwen4-exp shapes S={S}")
+    H, E, K, I, SI = 4096, 512, 10, 512, 4096
+    L = moe.Layer.load(950, moe.dims(H, E, K, I, SI), np.zeros((E, H), np.float32))
+    L.synth(seed=777)
+    host = dict(dims=dict(hidden=H, experts=E, topk=K, inter=I, shared_inter=SI, norm_topk=1),
+                router=L.read_router(), experts=[L.read_expert(e) for e in range(E)], shared=L.read_shared())
+    Lo = oracle_lib.OracleLayer(host)
+    err = _check_forward(L, Lo, synth.hidden_states(S, H, seed=S + 1), f"qwen4 S={S}")
+    say(f"  rel L2 {err:.2e}")
