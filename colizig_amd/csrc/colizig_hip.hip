@@ -342,33 +342,39 @@ void launch_up(const StepArgs &A, hipStream_t st) {
     }
 }
 
-template <int NBI, int NBS>
+template <int NJ, int NJS>
 void launch_down_t(const StepArgs &A, hipStream_t st) {
     const uint32_t blocks = (uint32_t)A.S * ((A.L.H + 3) / 4);
-    k_down_fast<NBI, NBS, kDownKC><<<blocks, 256, 0, st>>>(A);
+    if (A.L.K > kDownKC && A.L.K % 5 == 0 && A.L.K <= 20)  // e.g. top-10: two batches of 5
+        k_down_fast<NJ, NJS, 5><<<blocks, 256, 0, st>>>(A);
+    else
+        k_down_fast<NJ, NJS, kDownKC><<<blocks, 256, 0, st>>>(A);
 }
 
-template <int NBI>
+template <int NJ>
 bool launch_down_s(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
-    if (L.SI == 0) { launch_down_t<NBI, 0>(A, st); return true; }
-    switch ((L.SI % 64) ? 0u : L.SI / 64) {
-        case 8: launch_down_t<NBI, 8>(A, st); return true;
-        case 16: launch_down_t<NBI, 16>(A, st); return true;
-        case 32: launch_down_t<NBI, 32>(A, st); return true;
-        case 64: launch_down_t<NBI, 64>(A, st); return true;
+    if (L.SI == 0) { launch_down_t<NJ, 0>(A, st); return true; }
+    switch ((L.SI % 256) ? 0u : L.SI / 256) {
+        case 1: launch_down_t<NJ, 1>(A, st); return true;
+        case 2: launch_down_t<NJ, 2>(A, st); return true;
+        case 4: launch_down_t<NJ, 4>(A, st); return true;
+        case 8: launch_down_t<NJ, 8>(A, st); return true;
+        case 16: launch_down_t<NJ, 16>(A, st); return true;
         default: return false;
     }
 }
 
+// fast path for I = 256 * {1, 2, 3, 4} and SI = 256 * {0, 1, 2, 4, 8, 16},
+// generic kernel otherwise
 void launch_down(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
     bool ok = false;
-    switch ((L.I % 64) ? 0u : L.I / 64) {
+    switch ((L.I % 256) ? 0u : L.I / 256) {
+        case 1: ok = launch_down_s<1>(A, st); break;
+        case 2: ok = launch_down_s<2>(A, st); break;
+        case 3: ok = launch_down_s<3>(A, st); break;
         case 4: ok = launch_down_s<4>(A, st); break;
-        case 8: ok = launch_down_s<8>(A, st); break;
-        case 12: ok = launch_down_s<12>(A, st); break;
-        case 16: ok = launch_down_s<16>(A, st); break;
         default: break;
     }
     if (!ok) {

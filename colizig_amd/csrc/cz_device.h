@@ -67,6 +67,16 @@ __host__ __device__ inline float cz_sigmoid(float x) {
 // activation.zig:18-20
 __host__ __device__ inline float cz_silu(float x) { return x * cz_sigmoid(x); }
 
+// The same two-branch silu on the hardware exponential and reciprocal
+// (v_exp_f32, v_rcp_f32: about 1 ulp each).  The expert activations use it:
+// their results are held to a relative L2 of 1e-3, not to the bit, while
+// routing keeps the correctly rounded cz_expf.
+__device__ inline float cz_silu_fast(float x) {
+    const float z = __expf(-__builtin_fabsf(x));  // (0, 1]
+    const float r = __builtin_amdgcn_rcpf(1.0f + z);
+    return x * (x >= 0.0f ? r : z * r);
+}
+
 // ---------------------------------------------------------------------------
 // OCP E4M3 (e4m3fn) decode with gfx950's v_cvt_pk_f32_fp8: two bytes of a
 // dword per instruction, exact (every E4M3 value is an f32).  The dequantised

@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
         const uint32_t dst = s_rowdst[r];
         if (dst != ~0u) {
             float v;
-            if constexpr (MODE == GG_GATEUP) v = cz_silu(acc[0][i]) * acc[1][i];
+            if constexpr (MODE == GG_GATEUP) v = cz_silu_fast(acc[0][i]) * acc[1][i];
             else v = acc[0][i];
             P.c[(uint64_t)dst * P.N + n] = v;
         }

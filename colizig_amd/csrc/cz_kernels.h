@@ -684,7 +684,7 @@ __device__ inline void cz_up_rows(const StepArgs &A, const UpItem &it, const flo
         float au = cz_row_dot<NB>(du[rr], xv, su[rr]);
         ag = cz_wave_sum_dpp(ag);
         au = cz_wave_sum_dpp(au);
-        if (lane == (uint32_t)rr && r < it.rows) it.out[r] = cz_silu(ag) * au;
+        if (lane == (uint32_t)rr && r < it.rows) it.out[r] = cz_silu_fast(ag) * au;
     }
 }
 
@@ -701,60 +701,92 @@ __global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
 
 // ---------------------------------------------------------------------------
 // down + weighted combine (+ shared expert, + residual), fast path: one wave
-// per output row; routed row width I = 64*NBI, shared row width SI = 64*NBS
-// (NBS 0 = none).  Experts are taken KC at a time, every weight, scale and h
-// load of a chunk issued before its arithmetic.
+// per output row.  Lane l owns the column groups 4l + 256j (j < NJ), so every
+// load instruction of a row, its h slice and its scales covers whole
+// contiguous lines; group j of lane l lies in scale block 2j + l/32.  The h
+// slices of the first KC experts are requested before the token's routing is
+// read (they do not depend on it); the routing is read as wave-uniform values,
+// so the weight addresses are scalar.  I = 256*NJ, SI = 256*NJS (NJS 0 =
+// no shared expert).
 // ---------------------------------------------------------------------------
-template <int NBI, int NBS, int KC>
+template <int NJ>
+__device__ inline void cz_load_h_groups(const float *__restrict__ hrow, uint32_t lane, float (&hv)[NJ][4]) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const float4 v = *(const float4 *)(hrow + 4 * lane + 256 * j);
+        hv[j][0] = v.x; hv[j][1] = v.y; hv[j][2] = v.z; hv[j][3] = v.w;
+    }
+}
+
+template <int NJ>
+__device__ inline void cz_load_w_groups(const uint8_t *__restrict__ wrow, const float *__restrict__ srow, uint32_t lane,
+                                        uint32_t (&d)[NJ], float (&sc)[NJ]) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        d[j] = *(const uint32_t *)(wrow + 4 * lane + 256 * j);
+        sc[j] = srow[2 * j + (lane >> 5)];
+    }
+}
+
+// sum over the lane's groups of (e4m3 . h) * block scale
+template <int NJ>
+__device__ inline float cz_groups_dot(const uint32_t (&d)[NJ], const float (&hv)[NJ][4], const float (&sc)[NJ]) {
+    float p = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) p = __builtin_fmaf(cz_dot4_raw(d[j], hv[j], 0.0f), sc[j], p);
+    return p;
+}
+
+__device__ inline uint32_t cz_uniform_u32(const uint32_t *p) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)*p); }
+__device__ inline float cz_uniform_f32(const float *p) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, *p)));
+}
+
+template <int NJ, int NJS, int KC>
 __device__ inline void cz_down_row(const StepArgs &A, uint32_t tok, uint32_t r, uint32_t lane) {
-    constexpr int NDI = NBI / 4;
     const LayerDev &L = A.L;
-    const uint32_t col0 = lane * NBI;
-    // the token's K expert ids and gates, one per lane, broadcast by readlane
-    const uint32_t my_e = lane < L.K ? A.idx[(uint64_t)tok * L.K + lane] : 0u;
-    const float my_g = lane < L.K ? A.gates[(uint64_t)tok * L.K + lane] : 0.0f;
+    const uint64_t slot0 = (uint64_t)tok * L.K;
+    float hv[KC][NJ][4];
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+        cz_load_h_groups<NJ>(A.h + (slot0 + min((uint32_t)c, L.K - 1)) * L.I, lane, hv[c]);
     float acc = 0.0f;
     for (uint32_t z0 = 0; z0 < L.K; z0 += KC) {
-        uint32_t dd[KC][NDI];
-        RowScales<NBI> sd[KC];
-        float hv[KC][NBI];
+        if (z0 > 0) {
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const uint32_t z = min(z0 + c, L.K - 1);
-            const uint32_t e = min((uint32_t)__builtin_amdgcn_readlane((int)my_e, z), L.E - 1);
-            const uint64_t sl = cz_slot(L, e);
-            const uint8_t *Wd = L.ew + sl * L.ew_stride + 2ull * L.I * L.H;
-            cz_load_row<NBI>(Wd + (uint64_t)r * L.I + col0, dd[c]);
-            cz_load_scales<NBI>(L.es + sl * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI,
-                                col0, sd[c]);
+            for (int c = 0; c < KC; ++c)
+                cz_load_h_groups<NJ>(A.h + (slot0 + min(z0 + c, L.K - 1)) * L.I, lane, hv[c]);
         }
+        uint32_t dd[KC][NJ];
+        float sc[KC][NJ];
+        float gz[KC];
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
             const uint32_t z = min(z0 + c, L.K - 1);
-            cz_load_x<NBI>(A.h + (uint64_t)(tok * L.K + z) * L.I + col0, hv[c]);
+            const uint32_t e = min(cz_uniform_u32(A.idx + slot0 + z), L.E - 1);
+            gz[c] = cz_uniform_f32(A.gates + slot0 + z);
+            const uint64_t sl = cz_slot(L, e);
+            cz_load_w_groups<NJ>(L.ew + sl * L.ew_stride + 2ull * L.I * L.H + (uint64_t)r * L.I,
+                                 L.es + sl * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI, lane,
+                                 dd[c], sc[c]);
         }
         __builtin_amdgcn_sched_barrier(0);  // the chunk's loads are all in flight
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-            const uint32_t z = min(z0 + c, L.K - 1);
-            const float g = cz_readlane(my_g, z);
-            const float p = cz_row_dot<NBI>(dd[c], hv[c], sd[c]);
-            if (z0 + c < L.K) acc = __builtin_fmaf(g, p, acc);
+            const float p = cz_groups_dot<NJ>(dd[c], hv[c], sc[c]);
+            if (z0 + c < L.K) acc = __builtin_fmaf(gz[c], p, acc);
         }
     }
-    if constexpr (NBS > 0) {
-        constexpr int NDS = NBS / 4;
-        const uint32_t cs0 = lane * NBS;
-        uint32_t dd[NDS];
-        RowScales<NBS> ss;
-        cz_load_row<NBS>(L.sw + 2ull * L.SI * L.H + (uint64_t)r * L.SI + cs0, dd);
-        cz_load_scales<NBS>(L.ss + 2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI, cs0, ss);
-        float hv[NBS];
-        cz_load_x<NBS>(A.hs + (uint64_t)tok * L.SI + cs0, hv);
-        const float sgv = A.sgate[tok];
+    if constexpr (NJS > 0) {
+        float hs[NJS][4];
+        uint32_t ds[NJS];
+        float ss[NJS];
+        cz_load_h_groups<NJS>(A.hs + (uint64_t)tok * L.SI, lane, hs);
+        cz_load_w_groups<NJS>(L.sw + 2ull * L.SI * L.H + (uint64_t)r * L.SI,
+                              L.ss + 2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI, lane, ds, ss);
+        const float sgv = cz_uniform_f32(A.sgate + tok);
         __builtin_amdgcn_sched_barrier(0);
-        const float p = cz_row_dot<NBS>(dd, hv, ss);
-        acc = __builtin_fmaf(sgv, p, acc);
+        acc = __builtin_fmaf(sgv, cz_groups_dot<NJS>(ds, hs, ss), acc);
     }
     const float tot = cz_wave_sum_dpp(acc);
     if (lane == 0) {
@@ -763,7 +795,7 @@ __device__ inline void cz_down_row(const StepArgs &A, uint32_t tok, uint32_t r, 
     }
 }
 
-template <int NBI, int NBS, int KC>
+template <int NJ, int NJS, int KC>
 __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -771,7 +803,7 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
     const uint32_t tok = blockIdx.x / tiles_h, tile = blockIdx.x - tok * tiles_h;
     const uint32_t r = tile * 4 + wave;
     if (r >= L.H || tok >= (uint32_t)A.S) return;
-    cz_down_row<NBI, NBS, KC>(A, tok, r, lane);
+    cz_down_row<NJ, NJS, KC>(A, tok, r, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -801,7 +833,7 @@ __global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
     float au = cz_dot_fp8_strided(it.Wu + (uint64_t)r * L.H, it.Su + (uint64_t)(r / CZ_BLOCK) * L.nbH, xs, L.H, lane);
     ag = cz_wave_sum_dpp(ag);
     au = cz_wave_sum_dpp(au);
-    if (lane == 0) it.out[r] = cz_silu(ag) * au;
+    if (lane == 0) it.out[r] = cz_silu_fast(ag) * au;
 }
 
 __global__ __launch_bounds__(256) void k_down_generic(StepArgs A) {
