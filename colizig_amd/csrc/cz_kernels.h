@@ -387,13 +387,12 @@ __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
 // ---------------------------------------------------------------------------
 // routing of one token by one wave (moe.zig:435-463): mx = max logit; v =
 // exp(l - mx) in f32; K passes of a strict '>' scan over the unchosen from
-// bv = -1 (ties to the lowest id; none left -> expert 0); top = sum of the
-// picked v in f64 in pick order; den = norm_topk ? top : sum_e f64(v_e) in
-// expert order; gate_z = f32(f64(v_z) / den).  Lane l holds experts
-// l + 64m for m < M (M = ceil(E/64)); values move between lanes by DPP,
-// readlane and ballot only.  Lane z < K leaves pick z in registers (o_pos =
-// z, o_id, o_gate) and writes s_idx[z] / s_gate[z] (LDS), which the block
-// reads after a barrier.  Must be called by a whole wave.
+// bv = -1 (ties to the lowest id; none left -> expert 0); top = sum of the picked v in f64 in pick order; den = norm_topk ?
+// top : sum_e f64(v_e) in expert order; gate_z = f32(f64(v_z) / den).  Lane l
+// holds experts l + 64m for m < M (M = ceil(E/64)); values move between lanes
+// by DPP, readlane and ballot only.  Lane z < K leaves pick z in registers
+// (o_pos = z, o_id, o_gate) and writes s_idx[z] / s_gate[z] (LDS), which the
+// block reads after a barrier.  Must be called by a whole wave.
 // ---------------------------------------------------------------------------
 template <int M>
 __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
@@ -478,10 +477,12 @@ struct UpItem {
 };
 
 // Resolves block `blk` of a gate/up grid (rows_wg rows per block): routed
-// blocks [0, S*K*tiles_r) run the routing prologue (wave 0) and publish the
-// token's routing from the slot-0 tile-0 block; shared-expert blocks follow,
-// and their tile-0 block computes the token's sigmoid gate.
-template <int M>
+// blocks [0, S*K*tiles_r) route their token (wave 0) and publish the token's routing from the slot-0 tile-0
+// block; shared-expert blocks follow, and their tile-0 block computes the
+// token's sigmoid gate.  With xs_lds, the token's row of the router input is
+// staged in LDS: every thread requests its NXR float4 of it before the
+// routing and stores them after it (H/4 <= 256*NXR).
+template <int M, int NXR>
 __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const float *xn, float4 *xs_lds = nullptr) {
     const LayerDev &L = A.L;
     __shared__ uint32_t s_idx[CZ_MAX_K];
@@ -491,35 +492,36 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
     const uint32_t nslots = (uint32_t)A.S * L.K;
     uint32_t blk = blockIdx.x;
     UpItem it;
-    // the block's token row of the router input, staged in LDS while the
-    // routing runs (H/4 float4, H a multiple of 4): threads [first,
-    // blockDim) issue two loads at a time before storing them
-    auto stage_x = [&](uint32_t tok, uint32_t first) {
-        if (!xs_lds || threadIdx.x < first) return;
-        const float4 *src = (const float4 *)(xn + (uint64_t)tok * L.H);
-        const uint32_t n4 = L.H / 4, step = blockDim.x - first;
-        for (uint32_t i0 = threadIdx.x - first; i0 < n4; i0 += 2 * step) {
-            float4 r[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                if (i0 + q * step < n4) r[q] = src[i0 + q * step];
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                if (i0 + q * step < n4) xs_lds[i0 + q * step] = r[q];
-        }
-    };
+    const uint32_t n4 = L.H / 4;
+    float4 xr[NXR > 0 ? NXR : 1];
+#define CZ_UP_LOAD_X(tok_)                                                       \
+    if (NXR > 0 && xs_lds) {                                                     \
+        const float4 *src_ = (const float4 *)(xn + (uint64_t)(tok_) * L.H);      \
+        _Pragma("unroll") for (int q = 0; q < NXR; ++q) {                        \
+            const uint32_t i_ = threadIdx.x + 256u * q;                          \
+            xr[q] = i_ < n4 ? src_[i_] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);    \
+        }                                                                        \
+    }
+#define CZ_UP_STORE_X()                                                          \
+    if (NXR > 0 && xs_lds) {                                                     \
+        _Pragma("unroll") for (int q = 0; q < NXR; ++q) {                        \
+            const uint32_t i_ = threadIdx.x + 256u * q;                          \
+            if (i_ < n4) xs_lds[i_] = xr[q];                                     \
+        }                                                                        \
+    }
     if (blk < nslots * tiles_r) {
         const uint32_t slot = blk / tiles_r;
         it.tile = blk - slot * tiles_r;
         it.tok = slot / L.K;
         const uint32_t z = slot - it.tok * L.K;
-        stage_x(it.tok, 0);
+        CZ_UP_LOAD_X(it.tok)
+        const float *lg = A.logits + (uint64_t)it.tok * L.E;
         if (wave == 0) {
             uint32_t o_pos = 0, o_id = 0;
             float o_gate = 0.0f;
-            cz_route_wave_m<M>(A.logits + (uint64_t)it.tok * L.E, L.E, L.K, L.norm_topk, s_idx, s_gate, o_pos, o_id,
-                               o_gate);
+            cz_route_wave_m<M>(lg, L.E, L.K, L.norm_topk, s_idx, s_gate, o_pos, o_id, o_gate);
         }
+        CZ_UP_STORE_X()
         __syncthreads();
         if (z == 0 && it.tile == 0 && wave == 0) {
             for (uint32_t k = lane; k < L.K; k += 64) {
@@ -553,7 +555,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         it.out = A.hs + (uint64_t)it.tok * L.SI;
         it.rows = L.SI;
         it.routed = false;
-        stage_x(it.tok, 0);
+        CZ_UP_LOAD_X(it.tok)
         // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         if (it.tile == 0 && wave == 0) {
             const float *xs = xn + (uint64_t)it.tok * L.H;
@@ -565,8 +567,11 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
             d = cz_wave_sum_dpp(d);
             if (lane == 0) A.sgate[it.tok] = cz_sigmoid(d);
         }
+        CZ_UP_STORE_X()
         __syncthreads();
     }
+#undef CZ_UP_LOAD_X
+#undef CZ_UP_STORE_X
     return it;
 }
 
@@ -693,7 +698,7 @@ __global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
     __shared__ float4 xs[NB * 16];  // the token's router input, H = 64*NB floats
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xn = A.rms ? A.xn : A.x;
-    const UpItem it = cz_up_item<M>(A, 4 * RW, xn, xs);
+    const UpItem it = cz_up_item<M, (NB * 16 + 255) / 256>(A, 4 * RW, xn, xs);
     const uint32_t r0 = it.tile * 4 * RW + wave * RW;
     if (r0 >= it.rows) return;
     cz_up_rows<NB, RW>(A, it, (const float *)xs, r0, lane);
@@ -825,7 +830,7 @@ __global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xn = A.rms ? A.xn : A.x;
-    const UpItem it = cz_up_item<M>(A, 4, xn);
+    const UpItem it = cz_up_item<M, 0>(A, 4, xn);
     const uint32_t r = it.tile * 4 + wave;
     if (r >= it.rows) return;
     const float *xs = xn + (uint64_t)it.tok * L.H;
