@@ -104,8 +104,10 @@ struct Work {
     uint32_t *counts = nullptr, *offsets = nullptr, *sorted_slot = nullptr, *slot_pos = nullptr,
              *tok_order = nullptr, *tile_expert = nullptr, *tile_row0 = nullptr, *ntiles = nullptr;
     float *o = nullptr, *os = nullptr;
+    _Float16 *xh = nullptr, *xl = nullptr, *hh = nullptr, *hl = nullptr, *hsh = nullptr, *hsl = nullptr;
     size_t cap_counts = 0, cap_offsets = 0, cap_sorted = 0, cap_slot_pos = 0, cap_tok_order = 0, cap_tiles = 0,
-           cap_tiles2 = 0, cap_ntiles = 0, cap_o = 0, cap_os = 0;
+           cap_tiles2 = 0, cap_ntiles = 0, cap_o = 0, cap_os = 0, cap_xh = 0, cap_xl = 0, cap_hh = 0, cap_hl = 0,
+           cap_hsh = 0, cap_hsl = 0;
 };
 
 // ---- HBM expert pool of the streaming tier: fixed-size slots (one expert's
@@ -247,7 +249,11 @@ int ensure_work_grouped(const colizig_dims &d, int S) {
         grow(&w.sorted_slot, &w.cap_sorted, sk) || grow(&w.slot_pos, &w.cap_slot_pos, sk) ||
         grow(&w.tok_order, &w.cap_tok_order, sk) || grow(&w.tile_expert, &w.cap_tiles, mt) ||
         grow(&w.tile_row0, &w.cap_tiles2, mt) || grow(&w.ntiles, &w.cap_ntiles, (size_t)1) ||
-        grow(&w.o, &w.cap_o, sk * d.hidden) || grow(&w.os, &w.cap_os, std::max<size_t>(1, s * d.hidden))) {
+        grow(&w.o, &w.cap_o, sk * d.hidden) || grow(&w.os, &w.cap_os, std::max<size_t>(1, s * d.hidden)) ||
+        grow(&w.xh, &w.cap_xh, s * d.hidden) || grow(&w.xl, &w.cap_xl, s * d.hidden) ||
+        grow(&w.hh, &w.cap_hh, sk * d.inter) || grow(&w.hl, &w.cap_hl, sk * d.inter) ||
+        grow(&w.hsh, &w.cap_hsh, std::max<size_t>(1, s * d.shared_inter)) ||
+        grow(&w.hsl, &w.cap_hsl, std::max<size_t>(1, s * d.shared_inter))) {
         snprintf(g_err, sizeof g_err, "grouped scratch allocation failed (S=%d)", S);
         return -2;
     }
@@ -256,7 +262,7 @@ int ensure_work_grouped(const colizig_dims &d, int S) {
 
 
 bool grouped_ok(const colizig_dims &d, int S) {
-    return S >= kGroupedMinTokens && d.hidden % 128 == 0 && d.inter % 128 == 0 && d.shared_inter % 128 == 0 &&
+    return S >= kGroupedMinTokens && d.hidden % 256 == 0 && d.inter % 128 == 0 && d.shared_inter % 128 == 0 &&
            (size_t)S * d.topk <= CZ_DISPATCH_MAX;
 }
 
@@ -426,7 +432,9 @@ int launch_step(const StepArgs &A, hipStream_t st, int which = kAll) {
 // a dense problem), combine.
 // grid of a grouped GEMM: M-tiles rounded up to whole groups of 8 (one per
 // XCD) times the N-tiles; workgroups past the real M-tiles exit
-uint32_t gg_blocks(uint32_t mtiles, uint32_t N) { return ((mtiles + 7) / 8) * 8 * (N / CZ_GG_N); }
+// grid of a grouped GEMM: 8 x ceil(items / 8) workgroups for at most mtiles
+// M-tiles x (N / cols) column tiles
+uint32_t gg_blocks(uint32_t mtiles, uint32_t N, uint32_t cols) { return (mtiles * (N / cols) + 7) / 8 * 8; }
 
 template <int M>
 void launch_route_tokens(const GroupArgs &G, hipStream_t st) {
@@ -458,9 +466,13 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.tile_row0 = w.tile_row0;
     G.ntiles = w.ntiles;
     G.max_tiles = grouped_max_tiles(Lh.d, S);
-    G.h = w.h;
+    G.xh = w.xh;
+    G.xl = w.xl;
+    G.hh = w.hh;
+    G.hl = w.hl;
+    G.hsh = w.hsh;
+    G.hsl = w.hsl;
     G.o = w.o;
-    G.hs = w.hs;
     G.os = w.os;
     G.xres = xres;
     G.out = out;
@@ -484,10 +496,13 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     P.N = L.I;
     P.Kd = L.H;
     P.nbK = L.nbH;
-    P.a = G.xn;
-    P.c = w.h;
+    P.a_hi = w.xh;
+    P.a_lo = w.xl;
+    P.c_hi = w.hh;
+    P.c_lo = w.hl;
     P.routed = 1;
-    k_gg<GG_GATEUP><<<gg_blocks(G.max_tiles, L.I), 256, 0, st>>>(G, P);
+    constexpr uint32_t cu = cz_gg_cols<GG_GATEUP>(), cd = cz_gg_cols<GG_DOWN>();
+    k_gg<GG_GATEUP><<<gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P);
     if (L.SI) {
         GGProblem Q = P;
         Q.w0 = L.sw;
@@ -497,10 +512,11 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.w1_off = (uint64_t)L.SI * L.H;
         Q.s1_off = (uint64_t)L.nbSI * L.nbH;
         Q.N = L.SI;
-        Q.c = w.hs;
+        Q.c_hi = w.hsh;
+        Q.c_lo = w.hsl;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
-        k_gg<GG_GATEUP><<<gg_blocks(mts, L.SI), 256, 0, st>>>(G, Q);
+        k_gg<GG_GATEUP><<<gg_blocks(mts, L.SI, cu), 256, 0, st>>>(G, Q);
     }
     // down
     GGProblem D{};
@@ -511,10 +527,11 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     D.N = L.H;
     D.Kd = L.I;
     D.nbK = L.nbI;
-    D.a = w.h;
+    D.a_hi = w.hh;
+    D.a_lo = w.hl;
     D.c = w.o;
     D.routed = 1;
-    k_gg<GG_DOWN><<<gg_blocks(G.max_tiles, L.H), 256, 0, st>>>(G, D);
+    k_gg<GG_DOWN><<<gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D);
     if (L.SI) {
         GGProblem Q = D;
         Q.w0 = L.sw + 2ull * L.SI * L.H;
@@ -523,11 +540,12 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.s_stride = 0;
         Q.Kd = L.SI;
         Q.nbK = L.nbSI;
-        Q.a = w.hs;
+        Q.a_hi = w.hsh;
+        Q.a_lo = w.hsl;
         Q.c = w.os;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
-        k_gg<GG_DOWN><<<gg_blocks(mts, L.H), 256, 0, st>>>(G, Q);
+        k_gg<GG_DOWN><<<gg_blocks(mts, L.H, cd), 256, 0, st>>>(G, Q);
     }
     k_combine<<<dim3((L.H + 255) / 256, S), 256, 0, st>>>(G);
     const hipError_t e = hipGetLastError();
@@ -652,7 +670,8 @@ extern "C" void colizig_cuda_shutdown(void) {
     for (void *p : {(void *)w.xin, (void *)w.out, (void *)w.xn, (void *)w.logits, (void *)w.gates,
                     (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx, (void *)w.counts, (void *)w.offsets,
                     (void *)w.sorted_slot, (void *)w.slot_pos, (void *)w.tok_order, (void *)w.tile_expert,
-                    (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os})
+                    (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os, (void *)w.xh, (void *)w.xl,
+                    (void *)w.hh, (void *)w.hl, (void *)w.hsh, (void *)w.hsl})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     StreamPool &P = g.pool;

@@ -28,12 +28,11 @@
 #include "cz_kernels.h"
 
 typedef _Float16 cz_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 cz_half4 __attribute__((ext_vector_type(4)));
 typedef float cz_float16v __attribute__((ext_vector_type(16)));
 
 #define CZ_GG_M 32        // rows (slots) per M-tile
-#define CZ_GG_N 128       // output columns per workgroup (4 waves x 32)
 #define CZ_GG_KB 128      // K block (= scale block)
-#define CZ_GG_LDS_ROW 136 // halves per LDS row (128 + 8 padding)
 
 struct GroupArgs {
     LayerDev L;
@@ -56,9 +55,10 @@ struct GroupArgs {
     uint32_t *ntiles;          // [1] M-tiles of the routed experts
     uint32_t max_tiles;
     // grouped GEMM buffers
-    float *h;                  // [S*K][I] sorted rows
+    _Float16 *xh, *xl;         // [S][H]    x as f16 hi + lo
+    _Float16 *hh, *hl;         // [S*K][I]  h of the sorted rows as f16 hi + lo
+    _Float16 *hsh, *hsl;       // [S][SI]   shared-expert h as f16 hi + lo
     float *o;                  // [S*K][H] sorted rows
-    float *hs;                 // [S][SI]
     float *os;                 // [S][H]
     const float *xres;         // [S][H] nullable
     float *out;                // [S][H]
@@ -97,6 +97,24 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
         rank += (eq < my_e || (eq == my_e && q < lane)) ? 1u : 0u;
     }
     if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + o_pos;
+    // the token's row of x as f16 hi + lo (x ~= hi + lo), the A operand of the
+    // gate/up GEMMs
+    {
+        const float *xs = G.xn + (uint64_t)t * L.H;
+        _Float16 *xh = G.xh + (uint64_t)t * L.H, *xl = G.xl + (uint64_t)t * L.H;
+        for (uint32_t i = 4 * lane; i < L.H; i += 256) {
+            const float4 v = *(const float4 *)(xs + i);
+            const float f[4] = {v.x, v.y, v.z, v.w};
+            cz_half4 hv, lv;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hv[q] = (_Float16)f[q];
+                lv[q] = (_Float16)(f[q] - (float)hv[q]);
+            }
+            *(cz_half4 *)(xh + i) = hv;
+            *(cz_half4 *)(xl + i) = lv;
+        }
+    }
     if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         const float *xs = G.xn + (uint64_t)t * L.H;
         float d = 0.0f;
@@ -220,7 +238,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
 // 8 E4M3 bytes (two dwords) -> 8 f16, exact: every E4M3 value is an f16,
 // and gfx950's v_cvt_scalef32_pk_f16_fp8 with scale 1.0 converts two bytes
 // of a dword per instruction (word_sel picks bytes 0-1 or 2-3)
-__device__ inline cz_half8 cz_fp8x8_to_f16(uint32_t w0, uint32_t w1) {
+__device__ __forceinline__ cz_half8 cz_fp8x8_to_f16(uint32_t w0, uint32_t w1) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, false);
     const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, true);
@@ -242,189 +260,218 @@ struct GGProblem {
     uint64_t s_stride;      // floats between experts
     uint64_t w1_off;        // GATEUP: up matrix offset from gate (bytes), scales likewise
     uint64_t s1_off;
-    uint32_t N, Kd;         // output columns, reduction length (both multiples of 128)
+    uint32_t N, Kd;         // output columns, reduction length (N % 256 == 0 for DOWN, Kd % 128 == 0)
     uint32_t nbK;           // scale blocks along K (= Kd/128)
-    const float *a;         // A rows: GATEUP xn [S][H] (row = token), DOWN h [rows][Kd]
-    float *c;               // C rows [rows][N]
+    const _Float16 *a_hi;   // A rows as f16 hi/lo: GATEUP x [S][H] (row = token), DOWN h [rows][Kd]
+    const _Float16 *a_lo;
+    _Float16 *c_hi;         // GATEUP: h rows as f16 hi/lo [rows][N]
+    _Float16 *c_lo;
+    float *c;               // DOWN: O rows [rows][N]
     int routed;             // 1: tiles from the dispatch table; 0: shared (rows = tokens in order)
     uint32_t rows_total;    // shared: S
 };
 
+// Output columns of one workgroup: 4 waves x 2 subtiles of 32 columns.  A
+// GATEUP wave's two subtiles are the gate and up columns of the same 32
+// outputs; a DOWN wave's are 64 adjacent columns.
 template <int MODE>
-__global__ __launch_bounds__(256) void k_gg(GroupArgs G, GGProblem P) {
-    constexpr int NMAT = MODE == GG_GATEUP ? 2 : 1;
-    __shared__ _Float16 a_hi[2][CZ_GG_M * CZ_GG_LDS_ROW];
-    __shared__ _Float16 a_lo[2][CZ_GG_M * CZ_GG_LDS_ROW];
-    __shared__ uint32_t s_rowsrc[CZ_GG_M];  // A row index of each tile row (~0u = padding)
-    __shared__ uint32_t s_rowdst[CZ_GG_M];  // C row index of each tile row
+__host__ __device__ constexpr uint32_t cz_gg_cols() { return MODE == GG_GATEUP ? 128u : 256u; }
 
-    const uint32_t lane = cz_lane(), wave = threadIdx.x >> 6, tid = threadIdx.x;
-    // XCD-aware order: workgroup b runs on XCD b % 8, so M-tile mt is pinned to
-    // XCD mt % 8 for all of its N-tiles and its A rows are read into one L2:
-    // b = ((mt / 8) * ntn + nt) * 8 + mt % 8
-    const uint32_t ntn = P.N / CZ_GG_N;
-    const uint32_t grp = blockIdx.x >> 3, mt = (grp / ntn) * 8 + (blockIdx.x & 7), nt = grp % ntn;
-    uint32_t e = 0, row0 = 0, rows = 0;
+// A tile of one K block in LDS: CZ_GG_M rows of 128 f16 (256 B = 16 chunks of
+// 16 B); chunk c of row r is stored at chunk c ^ (r & 15), so the 32 rows that
+// one MFMA operand read touches at one chunk lie in distinct banks.
+__device__ __forceinline__ uint32_t cz_gg_lds_off(uint32_t r, uint32_t c) { return r * 256u + ((c ^ (r & 15u)) << 4); }
+
+// A staging: thread t moves 32 B of row t/8 of the K block (logical chunks
+// 2(t%8) and 2(t%8)+1) of each of hi and lo: two 16-byte loads per array into
+// registers, stored to LDS after the current block's reads.  off is the
+// thread's byte offset of its chunks in the A arrays for K block 0 (padding
+// rows read row 0 of the problem; their results are not stored).
+struct CzA4 {
+    uint4 h0, h1, l0, l1;
+};
+__device__ __forceinline__ CzA4 cz_gg_load_a(const _Float16 *__restrict__ ahi, const _Float16 *__restrict__ alo,
+                                             uint32_t off, uint32_t kb) {
+    const uint64_t o = (uint64_t)kb * (CZ_GG_KB * 2u) + off;
+    const uint4 *ph = (const uint4 *)((const uint8_t *)ahi + o), *pl = (const uint4 *)((const uint8_t *)alo + o);
+    return CzA4{ph[0], ph[1], pl[0], pl[1]};
+}
+__device__ __forceinline__ void cz_gg_store_a(uint8_t *lds, uint32_t tid, const CzA4 &r) {
+    const uint32_t row = tid >> 3, c = 2u * (tid & 7u);
+    *(uint4 *)(lds + cz_gg_lds_off(row, c)) = r.h0;
+    *(uint4 *)(lds + cz_gg_lds_off(row, c + 1)) = r.h1;
+    *(uint4 *)(lds + CZ_GG_M * 256 + cz_gg_lds_off(row, c)) = r.l0;
+    *(uint4 *)(lds + CZ_GG_M * 256 + cz_gg_lds_off(row, c + 1)) = r.l1;
+}
+
+// One K block of a wave's 32 x (2 x 32) tile: 8 k-steps x 2 subtiles x (hi,
+// lo) MFMAs accumulated straight into acc, which holds the sum so far in
+// units of this block's scale.  Lane l's weights w[m][q] are bytes [64(l/32) +
+// 16q, +16) of its column's row in this K block; k-step s uses bytes
+// 8s..8s+7 of that half, so the A operand of row l%32 is logical chunk 8(l/32)
+// + s.  Step s+1's operands are fetched while step s multiplies.
+__device__ __forceinline__ void cz_gg_block(const uint8_t *lds_hi, const uint8_t *lds_lo, const uint4 (&w)[2][4],
+                                   cz_float16v (&acc)[2], uint32_t lane) {
+    const uint32_t rl = lane & 31u, ch = (lane >> 5) * 8u;
+    cz_half8 b[2][2], xh[2], xl[2];
+    auto fetch = [&](int s, int u) {
+        const uint32_t o = cz_gg_lds_off(rl, ch + s);
+        xh[u] = *(const cz_half8 *)(lds_hi + o);
+        xl[u] = *(const cz_half8 *)(lds_lo + o);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const uint4 wv = w[m][s >> 1];
+            b[u][m] = (s & 1) ? cz_fp8x8_to_f16(wv.z, wv.w) : cz_fp8x8_to_f16(wv.x, wv.y);
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int u = s & 1;
+        if (s < 7) fetch(s + 1, u ^ 1);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh[u], b[u][m], acc[m], 0, 0, 0);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl[u], b[u][m], acc[m], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Block scale of subtile m at K block kb, folded into acc: acc holds
+// sum_{j < kb} s_j P_j / cur; before block kb's products are added it is
+// multiplied by cur / s_kb, and at the end by the last scale, so the result is
+// sum_j s_j P_j with one extra rounding per block.  A zero scale makes the
+// block contribute 0: its weight bytes are cleared (E4M3 0x00 = +0) and cur is
+// kept.  sc and cur are wave-uniform.
+__device__ __forceinline__ void cz_gg_rescale(float sc, float &cur, cz_float16v &acc, uint4 (&w)[4]) {
+    const bool zero = sc == 0.0f;
+    const float r = (zero || cur == 0.0f) ? 1.0f : cur / sc;
+    cur = zero ? cur : sc;
+    const uint32_t keep = zero ? 0u : ~0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = make_uint4(w[q].x & keep, w[q].y & keep, w[q].z & keep, w[q].w & keep);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] *= r;
+}
+
+// Grouped GEMM: one M-tile (32 rows of one expert) x cz_gg_cols() output
+// columns per workgroup.  Work item t of the problem's T = tiles x column
+// tiles is mt = t / ntn, nt = t % ntn (an M-tile's column tiles are
+// consecutive); workgroup b runs on XCD b % 8 and takes item (b % 8) * ceil(T
+// / 8) + b / 8, so each XCD walks a contiguous range of items and an M-tile's
+// A rows are reused from its L2.  The next K block's A rows (f16 hi/lo, split
+// once by their producer) and weights are loaded into registers while this
+// block is multiplied; A goes through LDS (two buffers), weights straight
+// from HBM into the MFMA operands.  Several workgroups per CU hide the latency.
+template <int MODE>
+__global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
+    constexpr uint32_t NCOL = cz_gg_cols<MODE>();
+    // two LDS buffers of the A tile (hi at +0, lo at +CZ_GG_M*256)
+    __shared__ __align__(16) uint8_t lds0[2 * CZ_GG_M * 256], lds1[2 * CZ_GG_M * 256];
+    __shared__ uint32_t s_rowsrc[CZ_GG_M];  // A row of each tile row (padding: row 0 of the problem)
+    __shared__ uint32_t s_rowdst[CZ_GG_M];  // C row of each tile row (~0u = padding)
+
+    const uint32_t lane = cz_lane(), tid = threadIdx.x;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
+    const uint32_t ntn = P.N / NCOL;
+    const uint32_t mtiles = P.routed ? G.ntiles[0] : (P.rows_total + CZ_GG_M - 1) / CZ_GG_M;
+    const uint32_t T = mtiles * ntn, per = (T + 7) / 8;
+    const uint32_t j = blockIdx.x >> 3, t = (blockIdx.x & 7) * per + j;
+    if (j >= per || t >= T) return;  // block-uniform
+    const uint32_t mt = t / ntn, nt = t - mt * ntn;
+    uint32_t e = 0, row0, rows;
     if (P.routed) {
-        if (mt >= G.ntiles[0]) return;  // block-uniform
         e = G.tile_expert[mt];
         row0 = G.tile_row0[mt];
         rows = min((uint32_t)CZ_GG_M, G.offsets[e + 1] - row0);
     } else {
         row0 = mt * CZ_GG_M;
-        if (row0 >= P.rows_total) return;
         rows = min((uint32_t)CZ_GG_M, P.rows_total - row0);
     }
     if (tid < CZ_GG_M) {
-        uint32_t src = ~0u, dst = ~0u;
-        if (tid < rows) {
-            const uint32_t pos = row0 + tid;
-            dst = pos;
-            // GATEUP routed: the slot's token row of xn; DOWN routed: the sorted h row;
-            // shared: token rows in order
-            src = (MODE == GG_GATEUP && P.routed) ? G.sorted_slot[pos] / G.L.K : pos;
-        }
-        s_rowsrc[tid] = src;
-        s_rowdst[tid] = dst;
+        const uint32_t pos = row0 + min(tid, rows - 1);
+        // GATEUP routed: the slot's token row of x; DOWN routed: the sorted h
+        // row; shared: token rows in order
+        s_rowsrc[tid] = (MODE == GG_GATEUP && P.routed) ? G.sorted_slot[pos] / G.L.K : pos;
+        s_rowdst[tid] = tid < rows ? row0 + tid : ~0u;
     }
     __syncthreads();
+    // this thread's A chunks: row tid/8, logical chunks 2(tid%8), 2(tid%8)+1
+    const uint32_t aoff = (s_rowsrc[tid >> 3] * P.Kd + (tid & 7u) * 16u) * 2u;
 
     const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
     const uint8_t *W0 = P.w0 + sl * P.w_stride;
     const float *S0 = P.s0 + sl * P.s_stride;
-    // this wave's 32 output columns, this lane's weight row n and K half
-    const uint32_t n_base = nt * CZ_GG_N + wave * 32;
-    const uint32_t n = n_base + (lane & 31);
-    const uint32_t hk = (lane >> 5) * 64;
-    const uint8_t *wrow[NMAT];
-    const float *srow[NMAT];
+    // subtile m of this wave: its 32 columns, this lane's weight row n and K half
+    const uint8_t *wbase[2];
+    const float *srow[2];
+    uint32_t ncol[2], woff[2];
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-        wrow[m] = W0 + (m ? P.w1_off : 0) + (uint64_t)n * P.Kd + hk;
-        srow[m] = S0 + (m ? P.s1_off : 0) + (uint64_t)(n_base / CZ_BLOCK) * P.nbK;
+    for (int m = 0; m < 2; ++m) {
+        const uint32_t nb = MODE == GG_GATEUP ? nt * NCOL + wave * 32u : nt * NCOL + wave * 64u + 32u * m;
+        ncol[m] = nb + (lane & 31u);
+        const uint64_t moff = (MODE == GG_GATEUP && m) ? P.w1_off : 0;
+        const uint64_t soff = (MODE == GG_GATEUP && m) ? P.s1_off : 0;
+        wbase[m] = W0 + moff + (uint64_t)nb * P.Kd;                 // wave-uniform
+        woff[m] = (lane & 31u) * P.Kd + (lane >> 5) * 64u;          // per lane
+        srow[m] = S0 + soff + (uint64_t)(nb / CZ_BLOCK) * P.nbK;
     }
-    // A staging: thread tid loads row r = tid/8, 16 floats at column 16*(tid%8)
-    const uint32_t ar = tid >> 3, ac = (tid & 7) * 16;
-    const uint32_t asrc = s_rowsrc[ar];
-    const float *arow = asrc != ~0u ? P.a + (uint64_t)asrc * P.Kd + ac : nullptr;
-
-    cz_float16v acc[NMAT];
+    auto load_w = [&](uint32_t kb, uint4 (&w)[2][4]) {
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m)
+        for (int m = 0; m < 2; ++m) {
+            const uint4 *p = (const uint4 *)(wbase[m] + (uint64_t)kb * CZ_GG_KB + woff[m]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[m][q] = p[q];
+        }
+    };
+
+    cz_float16v acc[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
-
-    // K blocks kb+1 and kb+2 are in flight while kb is multiplied: weights in
-    // registers (two sets), the A rows of kb+1 staged to LDS at the end of
-    // iteration kb (double-buffered LDS)
-    uint4 wA[NMAT][4], wB[NMAT][4];
-    float4 aA[4], aB[4];
-    auto load_w = [&](uint32_t kb, uint4 (&w)[NMAT][4]) {
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[m][q] = ((const uint4 *)(wrow[m] + (uint64_t)kb * CZ_GG_KB))[q];
-    };
-    auto load_a = [&](uint32_t kb, float4 (&a)[4]) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            a[q] = arow ? ((const float4 *)(arow + (uint64_t)kb * CZ_GG_KB))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    // f32 -> f16 hi + lo (hi = f16(v), lo = f16(v - hi)), two 16-byte LDS
-    // stores per array
-    auto stage_a = [&](int buf, const float4 (&a)[4]) {
-        cz_half8 hv[2], lv[2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float v[4] = {a[q].x, a[q].y, a[q].z, a[q].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const _Float16 h = (_Float16)v[j];
-                hv[q >> 1][4 * (q & 1) + j] = h;
-                lv[q >> 1][4 * (q & 1) + j] = (_Float16)(v[j] - (float)h);
-            }
-        }
-        cz_half8 *hi = (cz_half8 *)(a_hi[buf] + ar * CZ_GG_LDS_ROW + ac);
-        cz_half8 *lo = (cz_half8 *)(a_lo[buf] + ar * CZ_GG_LDS_ROW + ac);
-        hi[0] = hv[0]; hi[1] = hv[1];
-        lo[0] = lv[0]; lo[1] = lv[1];
-    };
+    float cur[2] = {0.0f, 0.0f};
 
     const uint32_t nkb = P.Kd / CZ_GG_KB;  // >= 1
-    load_w(0, wA);
-    load_a(0, aA);
-    if (nkb > 1) {
-        load_w(1, wB);
-        load_a(1, aB);
-    }
-    stage_a(0, aA);
+    uint4 w[2][4], wn[2][4];
+    CzA4 an = cz_gg_load_a(P.a_hi, P.a_lo, aoff, 0);
+    load_w(0, w);
+    cz_gg_store_a(lds0, tid, an);
     __syncthreads();
     for (uint32_t kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        // this block's weights leave wA; wA then takes kb+2
-        uint4 wcur[NMAT][4];
+        const uint8_t *rd = (kb & 1) ? lds1 : lds0;
+        uint8_t *wr = (kb & 1) ? lds0 : lds1;
+        const float s0 = cz_const_f32(srow[0] + kb), s1 = cz_const_f32(srow[1] + kb);
+        // block kb+1 (the last block requests itself again): A rows and
+        // weights into registers
+        const uint32_t kn = min(kb + 1, nkb - 1);
+        an = cz_gg_load_a(P.a_hi, P.a_lo, aoff, kn);
+        load_w(kn, wn);
+        cz_gg_rescale(s0, cur[0], acc[0], w[0]);
+        cz_gg_rescale(s1, cur[1], acc[1], w[1]);
+        cz_gg_block(rd, rd + CZ_GG_M * 256, w, acc, lane);
+        cz_gg_store_a(wr, tid, an);
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+        for (int m = 0; m < 2; ++m)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wcur[m][q] = wA[m][q];
-        float sc[NMAT];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) sc[m] = srow[m][kb];
-        if (kb + 2 < nkb) {
-            load_w(kb + 2, wA);
-            load_a(kb + 2, aA);
-        }
-        cz_float16v part[NMAT];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) part[m][i] = 0.0f;
-        const _Float16 *ahi = a_hi[buf] + (lane & 31) * CZ_GG_LDS_ROW + hk;
-        const _Float16 *alo = a_lo[buf] + (lane & 31) * CZ_GG_LDS_ROW + hk;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const cz_half8 xh = *(const cz_half8 *)(ahi + 8 * s);
-            const cz_half8 xl = *(const cz_half8 *)(alo + 8 * s);
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                const uint4 wv = wcur[m][s >> 1];
-                const cz_half8 b = (s & 1) ? cz_fp8x8_to_f16(wv.z, wv.w) : cz_fp8x8_to_f16(wv.x, wv.y);
-                part[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, b, part[m], 0, 0, 0);
-                part[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, b, part[m], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[m][i] = __builtin_fmaf(sc[m], part[m][i], acc[m][i]);
-        if (kb + 1 < nkb) stage_a(buf ^ 1, aB);  // kb+1's rows (loaded an iteration ago)
-        // rotate: kb+1's weights/rows move to the A set's successor
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 t = wB[m][q];
-                wB[m][q] = wA[m][q];
-                wA[m][q] = t;
-            }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 t = aB[q];
-            aB[q] = aA[q];
-            aA[q] = t;
-        }
-        __syncthreads();
+            for (int q = 0; q < 4; ++q) w[m][q] = wn[m][q];
+        __syncthreads();  // block kb+1 is in LDS; buffer rd may be overwritten next
     }
-    // epilogue: lane holds rows (i/4)*8 + (l/32)*4 + i%4 of column n
+    // epilogue: lane holds rows (i/4)*8 + (l/32)*4 + i%4 of its columns
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const uint32_t r = (i / 4) * 8 + (lane >> 5) * 4 + (i % 4);
+        const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
         const uint32_t dst = s_rowdst[r];
-        if (dst != ~0u) {
-            float v;
-            if constexpr (MODE == GG_GATEUP) v = cz_silu_fast(acc[0][i]) * acc[1][i];
-            else v = acc[0][i];
-            P.c[(uint64_t)dst * P.N + n] = v;
+        if (dst == ~0u) continue;
+        if constexpr (MODE == GG_GATEUP) {
+            const float v = cz_silu_fast(acc[0][i] * cur[0]) * (acc[1][i] * cur[1]);
+            const _Float16 hi = (_Float16)v;
+            const uint64_t o = (uint64_t)dst * P.N + ncol[0];
+            P.c_hi[o] = hi;
+            P.c_lo[o] = (_Float16)(v - (float)hi);
+        } else {
+#pragma unroll
+            for (int m = 0; m < 2; ++m) P.c[(uint64_t)dst * P.N + ncol[m]] = acc[m][i] * cur[m];
         }
     }
 }

@@ -743,6 +743,11 @@ __device__ inline float cz_groups_dot(const uint32_t (&d)[NJ], const float (&hv)
 }
 
 __device__ inline uint32_t cz_uniform_u32(const uint32_t *p) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)*p); }
+// a wave-uniform read of memory no kernel in flight writes: through the
+// constant address space, i.e. a scalar load (lgkmcnt, not vmcnt)
+__device__ inline float cz_const_f32(const float *p) {
+    return *(const __attribute__((address_space(4))) float *)p;
+}
 __device__ inline float cz_uniform_f32(const float *p) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, *p)));
 }
