@@ -282,26 +282,30 @@ __host__ __device__ constexpr uint32_t cz_gg_cols() { return MODE == GG_GATEUP ?
 // one MFMA operand read touches at one chunk lie in distinct banks.
 __device__ __forceinline__ uint32_t cz_gg_lds_off(uint32_t r, uint32_t c) { return r * 256u + ((c ^ (r & 15u)) << 4); }
 
-// A staging: thread t moves 32 B of row t/8 of the K block (logical chunks
-// 2(t%8) and 2(t%8)+1) of each of hi and lo: two 16-byte loads per array into
-// registers, stored to LDS after the current block's reads.  off is the
-// thread's byte offset of its chunks in the A arrays for K block 0 (padding
-// rows read row 0 of the problem; their results are not stored).
+// A staging: the K block's 32 rows x 16 chunks of 16 B per array; thread t
+// moves chunks t and t + 256 (row j/16, logical chunk j%16) of each of hi and
+// lo, so one wave instruction reads 4 whole 256-byte row segments.  The loads
+// go into registers and are stored to LDS after the current block's reads.
+// off[i] is the thread's byte offset of chunk t + 256i in the A arrays for K
+// block 0 (padding rows read row 0 of the problem; their results are not
+// stored).
 struct CzA4 {
     uint4 h0, h1, l0, l1;
 };
 __device__ __forceinline__ CzA4 cz_gg_load_a(const _Float16 *__restrict__ ahi, const _Float16 *__restrict__ alo,
-                                             uint32_t off, uint32_t kb) {
-    const uint64_t o = (uint64_t)kb * (CZ_GG_KB * 2u) + off;
-    const uint4 *ph = (const uint4 *)((const uint8_t *)ahi + o), *pl = (const uint4 *)((const uint8_t *)alo + o);
-    return CzA4{ph[0], ph[1], pl[0], pl[1]};
+                                             const uint32_t (&off)[2], uint32_t kb) {
+    const uint64_t o = (uint64_t)kb * (CZ_GG_KB * 2u);
+    const uint8_t *bh = (const uint8_t *)ahi + o, *bl = (const uint8_t *)alo + o;
+    return CzA4{*(const uint4 *)(bh + off[0]), *(const uint4 *)(bh + off[1]), *(const uint4 *)(bl + off[0]),
+                *(const uint4 *)(bl + off[1])};
 }
 __device__ __forceinline__ void cz_gg_store_a(uint8_t *lds, uint32_t tid, const CzA4 &r) {
-    const uint32_t row = tid >> 3, c = 2u * (tid & 7u);
-    *(uint4 *)(lds + cz_gg_lds_off(row, c)) = r.h0;
-    *(uint4 *)(lds + cz_gg_lds_off(row, c + 1)) = r.h1;
-    *(uint4 *)(lds + CZ_GG_M * 256 + cz_gg_lds_off(row, c)) = r.l0;
-    *(uint4 *)(lds + CZ_GG_M * 256 + cz_gg_lds_off(row, c + 1)) = r.l1;
+    const uint32_t j0 = tid, j1 = tid + 256u;
+    const uint32_t o0 = cz_gg_lds_off(j0 >> 4, j0 & 15u), o1 = cz_gg_lds_off(j1 >> 4, j1 & 15u);
+    *(uint4 *)(lds + o0) = r.h0;
+    *(uint4 *)(lds + o1) = r.h1;
+    *(uint4 *)(lds + CZ_GG_M * 256 + o0) = r.l0;
+    *(uint4 *)(lds + CZ_GG_M * 256 + o1) = r.l1;
 }
 
 // One K block of a wave's 32 x (2 x 32) tile: 8 k-steps x 2 subtiles x (hi,
@@ -396,8 +400,13 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
         s_rowdst[tid] = tid < rows ? row0 + tid : ~0u;
     }
     __syncthreads();
-    // this thread's A chunks: row tid/8, logical chunks 2(tid%8), 2(tid%8)+1
-    const uint32_t aoff = (s_rowsrc[tid >> 3] * P.Kd + (tid & 7u) * 16u) * 2u;
+    // this thread's A chunks j = tid, tid + 256: row j/16, logical chunk j%16
+    uint32_t aoff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t j = tid + 256u * i;
+        aoff[i] = (s_rowsrc[j >> 4] * P.Kd + (j & 15u) * 8u) * 2u;
+    }
 
     const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
     const uint8_t *W0 = P.w0 + sl * P.w_stride;
