@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by what the same
 # counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0):
 # 12422.1 KiB fetched, 24.1 KiB written per dispatch.
-UP_TRAFFIC_BYTES = int(round((12422.1 * 2.0 + 24.1) * 1024))
+UP_TRAFFIC_BYTES = int(round((12399.1 * 2.0 + 48.1) * 1024))
 
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
