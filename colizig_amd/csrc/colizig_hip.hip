@@ -1443,6 +1443,8 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     G.gates = w.gates;
     G.sgate = w.sgate;
     G.tok_order = w.tok_order;
+    G.xh = nullptr;  // routing only: the grouped regime below splits x itself
+    G.xl = nullptr;
     switch (cz_route_groups(A.L.E)) {
         case 1: launch_route_tokens<1>(G, st); break;
         case 2: launch_route_tokens<2>(G, st); break;

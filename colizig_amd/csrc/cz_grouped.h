@@ -98,8 +98,8 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     }
     if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + o_pos;
     // the token's row of x as f16 hi + lo (x ~= hi + lo), the A operand of the
-    // gate/up GEMMs
-    {
+    // gate/up GEMMs (callers that only route pass no split buffers)
+    if (G.xh && G.xl) {
         const float *xs = G.xn + (uint64_t)t * L.H;
         _Float16 *xh = G.xh + (uint64_t)t * L.H, *xl = G.xl + (uint64_t)t * L.H;
         for (uint32_t i = 4 * lane; i < L.H; i += 256) {
