@@ -279,6 +279,16 @@ void free_layer(LayerHost &L) {
 
 hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : g.stream; }
 
+// Device activations are read and written as float4: x_dev / out_dev must be
+// 16-byte aligned (hipMalloc'ed buffers always are).
+bool dev_aligned(const void *a, const void *b = nullptr) {
+    if ((((uintptr_t)a) | ((uintptr_t)b)) & 15u) {
+        snprintf(g_err, sizeof g_err, "device activation buffers must be 16-byte aligned");
+        return false;
+    }
+    return true;
+}
+
 // ---- launches of one layer ------------------------------------------------
 // Router token tile: tt tokens of H floats staged in LDS, kept <= 32 KiB.
 int router_tokens_per_tile(uint32_t H) {
@@ -292,8 +302,9 @@ enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
 
 void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
-    if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: 16-token tiles
-        k_router_tiled<<<dim3((L.E + 7) / 8, (A.S + CZ_RT_TOK - 1) / CZ_RT_TOK), 256, 0, st>>>(A);
+    if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
+        if (A.rms) k_rms_rows<<<(A.S + 3) / 4, 256, 0, st>>>(A);
+        k_router_tiled<<<dim3((L.E + CZ_RT_EXP - 1) / CZ_RT_EXP, (A.S + CZ_RT_TOK - 1) / CZ_RT_TOK), 256 * CZ_RT_TG, 0, st>>>(A);
         return;
     }
     const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);
@@ -443,9 +454,13 @@ void launch_route_tokens(const GroupArgs &G, hipStream_t st) {
 
 int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
                    float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
-    const StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
+    StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
     const LayerDev &L = A.L;
     Work &w = g.work;
+    if (rms) {  // the RMS rows kernel writes the f16 split of xn for the gate/up GEMMs
+        A.xh = w.xh;
+        A.xl = w.xl;
+    }
     launch_router(A, st);
     GroupArgs G{};
     G.L = L;
@@ -466,8 +481,8 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.tile_row0 = w.tile_row0;
     G.ntiles = w.ntiles;
     G.max_tiles = grouped_max_tiles(Lh.d, S);
-    G.xh = w.xh;
-    G.xl = w.xl;
+    G.xh = rms ? nullptr : w.xh;  // no RMS rows kernel: the routing kernel splits x
+    G.xl = rms ? nullptr : w.xl;
     G.hh = w.hh;
     G.hl = w.hl;
     G.hsh = w.hsh;
@@ -547,7 +562,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.rows_total = (uint32_t)S;
         k_gg<GG_DOWN><<<gg_blocks(mts, L.H, cd), 256, 0, st>>>(G, Q);
     }
-    k_combine<<<dim3((L.H + 255) / 256, S), 256, 0, st>>>(G);
+    k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_err, sizeof g_err, "grouped launch: %s", hipGetErrorString(e));
@@ -934,7 +949,7 @@ extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, i
                                            uint32_t *idx_dev, float *gates_dev, void *stream) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!g.inited || S < 1 || !x_dev || !out_dev) return -1;
+    if (!g.inited || S < 1 || !x_dev || !out_dev || !dev_aligned(x_dev, out_dev)) return -1;
     LayerHost *L = find_layer(layer);
     int rc = check_layer_ready(L, layer);
     if (rc) return rc;
@@ -1014,7 +1029,7 @@ extern "C" int colizig_hip_chain_decode(uint32_t layer0, uint32_t nlayers, float
                                         float *xn_trace, uint32_t *idx_trace, float *gates_trace, void *stream) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!g.inited || S < 1 || !x_dev || nlayers == 0) return -1;
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || !dev_aligned(x_dev)) return -1;
     return chain_enqueue(layer0, nlayers, x_dev, S, eps, xn_trace, idx_trace, gates_trace, pick_stream(stream));
 }
 
@@ -1022,7 +1037,7 @@ extern "C" int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlay
                                                   float eps) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!g.inited || S < 1 || !x_dev || nlayers == 0) return -1;
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || !dev_aligned(x_dev)) return -1;
     // allocate scratch before capture (no allocation inside a capture)
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
@@ -1230,7 +1245,7 @@ extern "C" int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers,
                                               int reps, float *us_out) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || reps < 1 || !us_out) return -1;
+    if (!g.inited || S < 1 || !x_dev || nlayers == 0 || reps < 1 || !us_out || !dev_aligned(x_dev)) return -1;
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
         int rc = check_layer_ready(L, layer0 + l);
@@ -1554,7 +1569,7 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     StreamPool &P = g.pool;
-    if (!g.inited || !P.on || S < 1 || !x_dev || nlayers == 0) return -1;
+    if (!g.inited || !P.on || S < 1 || !x_dev || nlayers == 0 || !dev_aligned(x_dev)) return -1;
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
         int rc = check_layer_ready(L, layer0 + l);

@@ -147,3 +147,34 @@ __device__ inline float cz_wave_max_dpp(float v) {
 }
 
 __device__ inline uint32_t cz_lane() { return threadIdx.x & (CZ_WAVE - 1); }
+
+// DPP move of an integer; lanes whose source lane does not exist (or whose
+// row is masked off) read 0.
+template <int CTRL, int ROWS = 0xF>
+__device__ inline uint32_t cz_dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (integers: the order of
+// the additions does not matter): row_shr 1, 2, 4, 8 inside each 16-lane row,
+// then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3.
+__device__ inline uint32_t cz_wave_incl_scan_u32(uint32_t v) {
+    v += cz_dpp_u32<0x111>(v);
+    v += cz_dpp_u32<0x112>(v);
+    v += cz_dpp_u32<0x114>(v);
+    v += cz_dpp_u32<0x118>(v);
+    v += cz_dpp_u32<0x142, 0xA>(v);
+    v += cz_dpp_u32<0x143, 0xC>(v);
+    return v;
+}
+
+// Inclusive prefix sum inside aligned groups of g lanes (g = 1, 2, 4, 8 or
+// 16, wave-uniform; a group lies inside one 16-lane row).
+__device__ inline uint32_t cz_group_incl_scan_u32(uint32_t v, uint32_t g) {
+    const uint32_t p = cz_lane() & (g - 1);
+    if (g > 1) { const uint32_t t = cz_dpp_u32<0x111>(v); v += p >= 1 ? t : 0u; }
+    if (g > 2) { const uint32_t t = cz_dpp_u32<0x112>(v); v += p >= 2 ? t : 0u; }
+    if (g > 4) { const uint32_t t = cz_dpp_u32<0x114>(v); v += p >= 4 ? t : 0u; }
+    if (g > 8) { const uint32_t t = cz_dpp_u32<0x118>(v); v += p >= 8 ? t : 0u; }
+    return v;
+}

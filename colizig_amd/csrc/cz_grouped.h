@@ -75,6 +75,20 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     const uint32_t lane = cz_lane(), wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * 4 + wave;
     if (t >= (uint32_t)G.S) return;  // wave-uniform
+    // the token's row of x as f16 hi + lo (x ~= hi + lo), the A operand of the
+    // gate/up GEMMs (callers that only route pass no split buffers): its first
+    // 256*XB columns are requested before the routing and split after it
+    constexpr uint32_t XB = 16;
+    const bool split = G.xh && G.xl;
+    const float *xrow = G.xn + (uint64_t)t * L.H;
+    float4 xv[XB];
+    if (split) {
+#pragma unroll
+        for (uint32_t q = 0; q < XB; ++q) {
+            const uint32_t i = 4 * lane + 256 * q;
+            xv[q] = i < L.H ? *(const float4 *)(xrow + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
     uint32_t o_pos = 0, o_id = 0;
     float o_gate = 0.0f;
     cz_route_wave_m<M>(G.logits + (uint64_t)t * L.E, L.E, L.K, L.norm_topk, s_idx[wave], s_gate[wave], o_pos, o_id,
@@ -97,22 +111,31 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
         rank += (eq < my_e || (eq == my_e && q < lane)) ? 1u : 0u;
     }
     if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + o_pos;
-    // the token's row of x as f16 hi + lo (x ~= hi + lo), the A operand of the
-    // gate/up GEMMs (callers that only route pass no split buffers)
-    if (G.xh && G.xl) {
-        const float *xs = G.xn + (uint64_t)t * L.H;
+    if (split) {
         _Float16 *xh = G.xh + (uint64_t)t * L.H, *xl = G.xl + (uint64_t)t * L.H;
-        for (uint32_t i = 4 * lane; i < L.H; i += 256) {
-            const float4 v = *(const float4 *)(xs + i);
-            const float f[4] = {v.x, v.y, v.z, v.w};
-            cz_half4 hv, lv;
+        for (uint32_t i0 = 0; i0 < L.H; i0 += 256 * XB) {
+            if (i0 != 0) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                hv[q] = (_Float16)f[q];
-                lv[q] = (_Float16)(f[q] - (float)hv[q]);
+                for (uint32_t q = 0; q < XB; ++q) {
+                    const uint32_t i = i0 + 4 * lane + 256 * q;
+                    xv[q] = i < L.H ? *(const float4 *)(xrow + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
             }
-            *(cz_half4 *)(xh + i) = hv;
-            *(cz_half4 *)(xl + i) = lv;
+#pragma unroll
+            for (uint32_t q = 0; q < XB; ++q) {
+                const uint32_t i = i0 + 4 * lane + 256 * q;
+                if (i < L.H) {
+                    const float f[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+                    cz_half4 hv, lv;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        hv[c] = (_Float16)f[c];
+                        lv[c] = (_Float16)(f[c] - (float)hv[c]);
+                    }
+                    *(cz_half4 *)(xh + i) = hv;
+                    *(cz_half4 *)(xl + i) = lv;
+                }
+            }
         }
     }
     if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
@@ -131,29 +154,54 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
 // dispatch: one workgroup of 1024 threads (16 waves) over the S*K slot ids
 // (S*K <= CZ_DISPATCH_MAX, E <= CZ_MAX_E).  Counts by LDS integer atomics
 // (order-independent), offsets by one prefix, then a stable placement in
-// rounds of 1024 slots: inside a wave, equal ids are ranked by ballot in lane
-// order; across the round's waves, per-expert running bases are prefixed in
-// wave order.  Within an expert, rows keep slot order.
+// rounds of R slots: a bitmap per expert marks the round's slots of that
+// expert (bit = slot - round start), an exclusive popcount prefix over each
+// expert's words gives every slot its rank among the round's equal ids in
+// slot order, and per-expert running bases carry the earlier rounds.  Within
+// an expert, rows keep slot order.  R is the largest power of two <= 8192
+// with E * R bits in CZ_DISPATCH_WORDS words (R >= 512 for E <= 1024).
 // ---------------------------------------------------------------------------
 #define CZ_DISPATCH_MAX 8192
+#define CZ_DISPATCH_WORDS 16384
 
 __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
     const LayerDev &L = G.L;
     const uint32_t E = L.E, SK = (uint32_t)G.S * L.K;
     __shared__ uint16_t s_slot_e[CZ_DISPATCH_MAX];
-    __shared__ uint16_t s_wcnt[16][CZ_MAX_E];  // this round's count per (wave, expert), then its base
+    // [E][R/32 + 1]: the round's slots of each expert, rows padded to an odd
+    // stride so the same word of different experts falls in different banks
+    __shared__ uint32_t s_bits[CZ_DISPATCH_WORDS + CZ_MAX_E];
+    __shared__ uint16_t s_pre[CZ_DISPATCH_WORDS + CZ_MAX_E];  // set bits of the expert's earlier words
     __shared__ uint32_t s_cnt[CZ_MAX_E];
     __shared__ uint32_t s_off[CZ_MAX_E + 1];
-    __shared__ uint32_t s_run[CZ_MAX_E];       // rows placed so far per expert
-    const uint32_t tid = threadIdx.x, lane = cz_lane(), wave = tid >> 6;
+    __shared__ uint32_t s_run[CZ_MAX_E];            // rows placed so far per expert
+    const uint32_t tid = threadIdx.x, lane = cz_lane();
+    uint32_t R = CZ_DISPATCH_MAX;
+    while (E * (R / 32u) > CZ_DISPATCH_WORDS) R >>= 1;
+    const uint32_t WPE = R / 32u;    // words per expert: 16..256, a power of two
+    const uint32_t TPE = WPE / 16u;  // threads per expert (16 words each): 1..16, a power of two
+    const uint32_t RS = WPE + 1u;    // row stride of s_bits / s_pre
+    // the slots' expert ids: all of a thread's loads in flight at once
+    // (SK <= CZ_DISPATCH_MAX = 8 * 1024; indices past SK re-read slot SK - 1,
+    // unconditionally, so the loads are not serialised by branches)
+    uint32_t ev[CZ_DISPATCH_MAX / 1024];
+#pragma unroll
+    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) ev[q] = G.idx[min(tid + 1024u * q, SK - 1)];
+#pragma unroll
+    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) ev[q] = min(ev[q], E - 1);
     for (uint32_t i = tid; i < E; i += blockDim.x) {
         s_cnt[i] = 0;
         s_run[i] = 0;
     }
-    for (uint32_t i = tid; i < 16 * CZ_MAX_E; i += blockDim.x) (&s_wcnt[0][0])[i] = 0;
-    for (uint32_t i = tid; i < SK; i += blockDim.x) s_slot_e[i] = (uint16_t)min(G.idx[i], E - 1);
     __syncthreads();
-    for (uint32_t i = tid; i < SK; i += blockDim.x) atomicAdd(&s_cnt[s_slot_e[i]], 1u);
+#pragma unroll
+    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) {
+        const uint32_t i = tid + 1024u * q;
+        if (i < SK) {
+            s_slot_e[i] = (uint16_t)ev[q];
+            atomicAdd(&s_cnt[ev[q]], 1u);
+        }
+    }
     __syncthreads();
     if (tid < 64) {  // one wave: exclusive prefix of counts and of M-tile counts
         uint32_t acc = 0, tacc = 0;
@@ -161,12 +209,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
             const uint32_t e = e0 + lane;
             const uint32_t c = e < E ? s_cnt[e] : 0u;
             const uint32_t tc = (c + CZ_GG_M - 1) / CZ_GG_M;
-            // inclusive scans over the 64 lanes (shuffles; tiny)
-            uint32_t ic = c, it = tc;
-            for (uint32_t off = 1; off < 64; off <<= 1) {
-                const uint32_t a = __shfl_up(ic, off, 64), b = __shfl_up(it, off, 64);
-                if (lane >= off) { ic += a; it += b; }
-            }
+            const uint32_t ic = cz_wave_incl_scan_u32(c), it = cz_wave_incl_scan_u32(tc);
             if (e < E) {
                 s_off[e] = acc + ic - c;
                 const uint32_t tile0 = tacc + it - tc;
@@ -178,8 +221,8 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
                     }
                 }
             }
-            acc += (uint32_t)__shfl(ic, 63, 64);
-            tacc += (uint32_t)__shfl(it, 63, 64);
+            acc += (uint32_t)__builtin_amdgcn_readlane((int)ic, 63);
+            tacc += (uint32_t)__builtin_amdgcn_readlane((int)it, 63);
         }
         if (lane == 0) {
             s_off[E] = acc;
@@ -191,43 +234,45 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
         G.offsets[e] = s_off[e];
         if (e < E) G.counts[e] = s_cnt[e];
     }
-    for (uint32_t r0 = 0; r0 < SK; r0 += blockDim.x) {
-        const uint32_t i = r0 + tid;
-        const bool valid = i < SK;
-        const uint32_t e = valid ? s_slot_e[i] : 0u;
-        // rank among the wave's equal ids, and the wave's count per id
-        uint32_t rank = 0;
-        bool pending = valid;
-        while (__ballot(pending)) {
-            const uint64_t pm = __ballot(pending);
-            const uint32_t leader = (uint32_t)__builtin_ctzll(pm);
-            const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)e, leader);
-            const uint64_t m = __ballot(pending && e == v);
-            if (pending && e == v) {
-                rank = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1ull));
-                pending = false;
+    const uint32_t nw = E * RS;  // bitmap words in use (<= CZ_DISPATCH_WORDS + CZ_MAX_E)
+    for (uint32_t r0 = 0; r0 < SK; r0 += R) {
+        const uint32_t n = min(R, SK - r0);
+        for (uint32_t x = tid; x < nw; x += blockDim.x) s_bits[x] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += blockDim.x)
+            atomicOr(&s_bits[s_slot_e[r0 + i] * RS + (i >> 5)], 1u << (i & 31u));
+        __syncthreads();
+        // thread tid < E*TPE covers words 16k .. 16k + 15 of expert tid / TPE
+        // (k = tid % TPE); the TPE threads of an expert are consecutive lanes
+        // of one 16-lane row, so their scan is a segmented DPP scan
+        {
+            const bool act = tid < E * TPE;
+            const uint32_t w0 = act ? (tid / TPE) * RS + 16u * (tid % TPE) : 0u;
+            uint32_t c[16], tot = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                c[q] = tot;
+                tot += act ? (uint32_t)__builtin_popcount(s_bits[w0 + q]) : 0u;
             }
-            if (lane == leader) s_wcnt[wave][v] = (uint16_t)__builtin_popcountll(m);
-        }
-        __syncthreads();
-        // per expert: bases of the round's waves in wave order
-        for (uint32_t x = tid; x < E; x += blockDim.x) {
-            uint32_t run = s_run[x];
-            for (uint32_t w = 0; w < 16; ++w) {
-                const uint32_t c = s_wcnt[w][x];
-                s_wcnt[w][x] = (uint16_t)run;  // this wave's base (fits: run < S*K <= 8192)
-                run += c;
+            const uint32_t incl = cz_group_incl_scan_u32(tot, TPE);
+            if (act) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) s_pre[w0 + q] = (uint16_t)(incl - tot + c[q]);  // < R <= 8192
             }
-            s_run[x] = run;
         }
         __syncthreads();
-        if (valid) {
-            const uint32_t pos = s_off[e] + s_wcnt[wave][e] + rank;
-            G.sorted_slot[pos] = i;
-            G.slot_pos[i] = pos;
+        for (uint32_t i = tid; i < n; i += blockDim.x) {
+            const uint32_t e = s_slot_e[r0 + i], w = e * RS + (i >> 5);
+            const uint32_t below = s_bits[w] & ((1u << (i & 31u)) - 1u);
+            const uint32_t pos = s_off[e] + s_run[e] + s_pre[w] + (uint32_t)__builtin_popcount(below);
+            G.sorted_slot[pos] = r0 + i;
+            G.slot_pos[r0 + i] = pos;
         }
         __syncthreads();
-        for (uint32_t x = tid; x < 16 * CZ_MAX_E; x += blockDim.x) (&s_wcnt[0][0])[x] = 0;
+        for (uint32_t e = tid; e < E; e += blockDim.x) {
+            const uint32_t w = e * RS + WPE - 1u;
+            s_run[e] += s_pre[w] + (uint32_t)__builtin_popcount(s_bits[w]);
+        }
         __syncthreads();
     }
 }
@@ -489,19 +534,61 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
 // combine: out[t][d] = xres + ((0 + sgate*os) + g_a*O_a) + g_b*O_b ... in
 // ascending expert id (moe.zig:633-662; shared first, moe.zig:614-630)
 // ---------------------------------------------------------------------------
+// One workgroup per (token, 1024 columns), 4 columns per thread (H % 4 == 0).
+// The token's slot positions and gates are wave-uniform scalar loads; each
+// batch of 8 slots has all its loads in flight before the sums.
+#define CZ_COMBINE_COLS 1024
+
+__device__ __forceinline__ uint32_t cz_const_u32(const uint32_t *p) {
+    return *(const __attribute__((address_space(4))) uint32_t *)p;
+}
+
 __global__ __launch_bounds__(256) void k_combine(GroupArgs G) {
     const LayerDev &L = G.L;
     const uint32_t t = blockIdx.y;
-    const uint32_t d = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t d = blockIdx.x * CZ_COMBINE_COLS + 4u * threadIdx.x;
     if (d >= L.H || t >= (uint32_t)G.S) return;
-    float ys = 0.0f;
-    if (L.SI != 0) ys = ys + G.sgate[t] * G.os[(uint64_t)t * L.H + d];
-    for (uint32_t z = 0; z < L.K; ++z) {
-        const uint32_t s = G.tok_order[(uint64_t)t * L.K + z];
-        const float g = G.gates[s];
-        const float v = G.o[(uint64_t)G.slot_pos[s] * L.H + d];
-        ys = ys + g * v;
+    const uint64_t H = L.H;
+    float4 ys = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (L.SI != 0) {
+        const float sg = G.sgate[t];
+        const float4 v = *(const float4 *)(G.os + t * H + d);
+        ys.x = ys.x + sg * v.x;
+        ys.y = ys.y + sg * v.y;
+        ys.z = ys.z + sg * v.z;
+        ys.w = ys.w + sg * v.w;
     }
-    const uint64_t o = (uint64_t)t * L.H + d;
-    G.out[o] = (G.xres ? G.xres[o] : 0.0f) + ys;
+    const uint32_t *order = G.tok_order + (uint64_t)t * L.K;
+    for (uint32_t z0 = 0; z0 < L.K; z0 += 8) {
+        // unconditional loads (slots past K re-read slot K - 1): the scalar
+        // index loads of all 8 slots are issued together, then the rows
+        uint32_t sl[8], pos[8];
+        float g[8];
+        float4 v[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) sl[q] = cz_const_u32(order + min(z0 + q, L.K - 1));
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            g[q] = cz_const_f32(G.gates + sl[q]);
+            pos[q] = cz_const_u32(G.slot_pos + sl[q]);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) v[q] = *(const float4 *)(G.o + (uint64_t)pos[q] * H + d);
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            if (z0 + q < L.K) {
+                ys.x = ys.x + g[q] * v[q].x;
+                ys.y = ys.y + g[q] * v[q].y;
+                ys.z = ys.z + g[q] * v[q].z;
+                ys.w = ys.w + g[q] * v[q].w;
+            }
+        }
+    }
+    const uint64_t o = t * H + d;
+    float4 r = G.xres ? *(const float4 *)(G.xres + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    r.x = r.x + ys.x;
+    r.y = r.y + ys.y;
+    r.z = r.z + ys.z;
+    r.w = r.w + ys.w;
+    *(float4 *)(G.out + o) = r;
 }

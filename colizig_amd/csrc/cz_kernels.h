@@ -68,6 +68,7 @@ struct StepArgs {
     uint32_t *idx_trace;   // nullable [S][K]
     float *gates_trace;    // nullable [S][K]
     float *xn_trace;       // nullable [S][H]
+    _Float16 *xh, *xl;     // nullable [S][H]: k_rms_rows also writes xn as f16 hi + lo (xn ~= hi + lo)
     int S;
     int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
     int rms;
@@ -274,94 +275,193 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
     }
 }
 
-// Many-token router (S > 1): 256 threads = 8 experts x 32 chains, a tile of
-// 16 tokens per workgroup.  Thread (expert e, chain j) keeps one accumulator
-// per token and walks H in chunks of 256 columns: the router elements of its
-// chain come straight from HBM/L2 into registers, the normalised input tile
-// through LDS.  Each chain accumulates in increasing column order, exactly as
-// the one-token kernel, and the same half-wave combine finishes each logit,
-// so logits are bit-identical to the decode router's.  H % 256 == 0.
-#define CZ_RT_TOK 16
+// Many-token router input (S > 1, rms = 1): one wave per token writes xn =
+// x / sqrt(mean(x^2) + eps) in the one-token router's order (lane l sums the
+// squares of columns l, l + 64, ... in increasing order, then the DPP wave
+// sum), and, when xh / xl are given, xn split into f16 hi + lo (the grouped
+// GEMM's A operand).  Rows of up to CZ_RMS_MAXB * 2048 columns stay in
+// registers, loaded at once; loads past H read column H - 64 + lane and add
+// +0 (ss >= 0, so ss + 0 = ss exactly).  Longer rows are read twice.
+#define CZ_RMS_PB 32   // columns per lane per batch
+#define CZ_RMS_MAXB 2  // register-resident batches
 
-__global__ __launch_bounds__(256) void k_router_tiled(StepArgs A) {
-    const LayerDev &L = A.L;
-    const uint32_t H = L.H, E = L.E;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
-    const uint32_t e = blockIdx.x * 8 + wave * 2 + half;
-    const uint32_t ec = min(e, E - 1);
-    const uint32_t t0 = blockIdx.y * CZ_RT_TOK;
-    const uint32_t nt = min((uint32_t)CZ_RT_TOK, (uint32_t)A.S - t0);
-    __shared__ float s_inv[CZ_RT_TOK];
-    __shared__ float s_x[CZ_RT_TOK][256];
-    // 1. per-token 1/rms: wave w handles tokens w, w+4, ... (same order as the
-    //    one-token kernel's lane-strided sum and DPP reduction)
-    for (uint32_t t = wave; t < CZ_RT_TOK; t += 4) {
-        float inv = 1.0f;
-        if (A.rms && t < nt) {
-            // 16 loads in flight per batch, squares summed in column order
-            const float *xs = A.x + (uint64_t)(t0 + t) * H + lane;
-            float ss = 0.0f;
-            for (uint32_t i0 = 0; i0 < H; i0 += 64 * 16) {
-                float v[16];
+__device__ __forceinline__ void cz_rms_store(const StepArgs &A, uint64_t o, float v) {
+    A.xn[o] = v;
+    if (A.xn_trace) A.xn_trace[o] = v;
+    if (A.xh) {
+        const _Float16 hv = (_Float16)v;
+        A.xh[o] = hv;
+        A.xl[o] = (_Float16)(v - (float)hv);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
+    const uint32_t H = A.L.H;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x * 4 + wave;
+    if (t >= (uint32_t)A.S) return;  // wave-uniform
+    const float *xs = A.x + (uint64_t)t * H;
+    const uint64_t row = (uint64_t)t * H;
+    const uint32_t nb = (H + 64 * CZ_RMS_PB - 1) / (64 * CZ_RMS_PB);
+    float ss = 0.0f;
+    if (nb <= CZ_RMS_MAXB) {
+        float v[CZ_RMS_MAXB][CZ_RMS_PB];
 #pragma unroll
-                for (int q = 0; q < 16; ++q) v[q] = i0 + 64 * q < H ? xs[i0 + 64 * q] : 0.0f;
+        for (uint32_t b = 0; b < CZ_RMS_MAXB; ++b)
+            if (b < nb) {
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    if (i0 + 64 * q < H) {
-                        const float sq = v[q] * v[q];
-                        ss = ss + sq;
-                    }
+                for (uint32_t q = 0; q < CZ_RMS_PB; ++q) v[b][q] = xs[min(64 * (CZ_RMS_PB * b + q), H - 64) + lane];
+            }
+#pragma unroll
+        for (uint32_t b = 0; b < CZ_RMS_MAXB; ++b)
+            if (b < nb) {
+#pragma unroll
+                for (uint32_t q = 0; q < CZ_RMS_PB; ++q) {
+                    const float sq = 64 * (CZ_RMS_PB * b + q) < H ? v[b][q] * v[b][q] : 0.0f;
+                    ss = ss + sq;
                 }
             }
-            ss = cz_wave_sum_dpp(ss);
-            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
-        }
-        if (lane == 0) s_inv[t] = inv;
-    }
-    __syncthreads();
-    float acc[CZ_RT_TOK];
+        ss = cz_wave_sum_dpp(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
 #pragma unroll
-    for (int t = 0; t < CZ_RT_TOK; ++t) acc[t] = 0.0f;
-    const float *wr = L.router + (uint64_t)ec * H + j;
-    const bool pub = A.rms && blockIdx.x == 0;
-    // chunk c's router elements and input column, in registers one chunk ahead
-    float w[8], xv[CZ_RT_TOK];
-    auto load_chunk = [&](uint32_t c0) {
+        for (uint32_t b = 0; b < CZ_RMS_MAXB; ++b)
+            if (b < nb) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = wr[c0 + 32 * i];
-#pragma unroll
-        for (int t = 0; t < CZ_RT_TOK; ++t)
-            xv[t] = (uint32_t)t < nt ? A.x[(uint64_t)(t0 + t) * H + c0 + tid] : 0.0f;
-    };
-    load_chunk(0);
-    for (uint32_t c0 = 0; c0 < H; c0 += 256) {
-        float wc[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) wc[i] = w[i];
-        // stage the normalised chunk: thread tid covers column tid of each token
-#pragma unroll
-        for (int t = 0; t < CZ_RT_TOK; ++t) {
-            const float v = A.rms ? xv[t] * s_inv[t] : xv[t];
-            if (pub && (uint32_t)t < nt) {
-                A.xn[(uint64_t)(t0 + t) * H + c0 + tid] = v;
-                if (A.xn_trace) A.xn_trace[(uint64_t)(t0 + t) * H + c0 + tid] = v;
+                for (uint32_t q = 0; q < CZ_RMS_PB; ++q) {
+                    const uint32_t i = 64 * (CZ_RMS_PB * b + q) + lane;
+                    if (i < H) cz_rms_store(A, row + i, v[b][q] * inv);
+                }
             }
-            s_x[t][tid] = v;
-        }
-        if (c0 + 256 < H) load_chunk(c0 + 256);  // next chunk in flight during this one's FMAs
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int t = 0; t < CZ_RT_TOK; ++t) acc[t] = __builtin_fmaf(s_x[t][32 * i + j], wc[i], acc[t]);
-        __syncthreads();
+        return;
     }
+    for (uint32_t i0 = 0; i0 < H; i0 += 64 * CZ_RMS_PB) {
+        float v[CZ_RMS_PB];
 #pragma unroll
-    for (int t = 0; t < CZ_RT_TOK; ++t) {
-        float lg = cz_router_combine(acc[t], j, hb);
-        if (L.router_bias) lg = lg + L.router_bias[ec];
-        if (j == 0 && e < E && (uint32_t)t < nt) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
+        for (uint32_t q = 0; q < CZ_RMS_PB; ++q) v[q] = xs[min(i0 + 64 * q, H - 64) + lane];
+#pragma unroll
+        for (uint32_t q = 0; q < CZ_RMS_PB; ++q) {
+            const float sq = i0 + 64 * q < H ? v[q] * v[q] : 0.0f;
+            ss = ss + sq;
+        }
+    }
+    ss = cz_wave_sum_dpp(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+    for (uint32_t i = lane; i < H; i += 64) cz_rms_store(A, row + i, xs[i] * inv);
+}
+
+// Many-token router (S > 1): a workgroup of CZ_RT_TG x 256 threads computes
+// CZ_RT_EXP experts x CZ_RT_TOK tokens.  Thread (token group g, half-wave hw
+// of its 256, lane j) owns experts 2hw, 2hw + 1 of the tile and tokens
+// [g*NTT, (g+1)*NTT); lane j is chain j: it accumulates columns j, j + 32, ...
+// in increasing order, exactly as the one-token kernel, so logits are
+// bit-identical to the decode router's.  The router elements come from
+// HBM/L2 into registers (a ring of CZ_RT_RING chunk sets, CZ_RT_RING - 1
+// 256-column chunks ahead); the input chunk goes through LDS (two buffers,
+// one barrier per chunk), and each LDS value feeds two FMAs.  The half-wave
+// combine (cz_router_combine's additions, same order) reads the 32 chain sums
+// from LDS, one thread per logit.  Input: xn when rms = 1 (k_rms_rows ran
+// first), else x.  H % 256 == 0.
+#define CZ_RT_TOK 16
+#define CZ_RT_EXP 16
+#define CZ_RT_TG 2       // token groups (256 threads each)
+#define CZ_RT_ACC_LD 36  // floats per (expert, token) row of chain sums (16 B aligned, b128 conflict-free)
+#define CZ_RT_RING 4     // register sets of chunk operands in flight
+
+__global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
+    constexpr uint32_t NTT = CZ_RT_TOK / CZ_RT_TG;  // tokens per thread
+    const LayerDev &L = A.L;
+    const uint32_t H = L.H, E = L.E;
+    const uint32_t tid = threadIdx.x, col = tid & 255, g = tid >> 8, hw = col >> 5, j = col & 31;
+    const uint32_t ea = min(blockIdx.x * CZ_RT_EXP + 2 * hw, E - 1), eb = min(blockIdx.x * CZ_RT_EXP + 2 * hw + 1, E - 1);
+    const uint32_t t0 = blockIdx.y * CZ_RT_TOK;
+    const uint32_t nt = min((uint32_t)CZ_RT_TOK, (uint32_t)A.S - t0);
+    constexpr uint32_t XBUF = 2 * CZ_RT_TOK * 256, ACCN = CZ_RT_EXP * CZ_RT_TOK * CZ_RT_ACC_LD;
+    __shared__ __align__(16) float s_buf[XBUF > ACCN ? XBUF : ACCN];
+    const float *src = A.rms ? A.xn : A.x;
+    const float *wa = L.router + (uint64_t)ea * H + j, *wb = L.router + (uint64_t)eb * H + j;
+    // this thread stages column `col` of tokens g*NTT .. g*NTT + NTT - 1 (clamped to nt - 1)
+    const float *xcol = src + (uint64_t)t0 * H + col;
+    float acc[2][NTT];
+#pragma unroll
+    for (uint32_t t = 0; t < NTT; ++t) acc[0][t] = acc[1][t] = 0.0f;
+    float w[CZ_RT_RING][2][8], xv[CZ_RT_RING][NTT];
+    const uint32_t nch = H / 256;
+    auto load_chunk = [&](uint32_t r, uint32_t c) {
+        const uint32_t c0 = min(c, nch - 1) * 256;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[r][0][i] = wa[c0 + 32 * i];
+            w[r][1][i] = wb[c0 + 32 * i];
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < NTT; ++t) xv[r][t] = xcol[(uint64_t)min(g * NTT + t, nt - 1) * H + c0];
+    };
+#pragma unroll
+    for (uint32_t r = 0; r + 1 < CZ_RT_RING; ++r) load_chunk(r, r);
+    for (uint32_t cb = 0; cb < nch; cb += CZ_RT_RING) {
+#pragma unroll
+        for (uint32_t r = 0; r < CZ_RT_RING; ++r) {
+            const uint32_t c = cb + r;
+            if (c < nch) {  // uniform
+                float *sx = s_buf + (c & 1) * (CZ_RT_TOK * 256);
+#pragma unroll
+                for (uint32_t t = 0; t < NTT; ++t) sx[(g * NTT + t) * 256 + col] = xv[r][t];
+                float wc[2][8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    wc[0][i] = w[r][0][i];
+                    wc[1][i] = w[r][1][i];
+                }
+                if (c + CZ_RT_RING - 1 < nch) load_chunk((r + CZ_RT_RING - 1) % CZ_RT_RING, c + CZ_RT_RING - 1);
+                __syncthreads();
+                const float *sxg = sx + g * NTT * 256 + j;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (uint32_t t = 0; t < NTT; ++t) {
+                        const float xval = sxg[t * 256 + 32 * i];
+                        acc[0][t] = __builtin_fmaf(xval, wc[0][i], acc[0][t]);
+                        acc[1][t] = __builtin_fmaf(xval, wc[1][i], acc[1][t]);
+                    }
+            }
+        }
+    }
+    __syncthreads();  // every thread is done with the input buffers
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (uint32_t t = 0; t < NTT; ++t)
+            s_buf[((2 * hw + m) * CZ_RT_TOK + g * NTT + t) * CZ_RT_ACC_LD + j] = acc[m][t];
+    __syncthreads();
+    if (tid >= CZ_RT_EXP * CZ_RT_TOK) return;
+    // thread (expert el = tid / 16, token t = tid % 16): total_l = ((0 + a_l)
+    // + a_{l+8}) + a_{l+16}) + a_{l+24}, sum = -0 + total_0 + ... + total_7
+    const uint32_t el = tid >> 4, t = tid & 15;
+    const float4 *row = (const float4 *)(s_buf + (el * CZ_RT_TOK + t) * CZ_RT_ACC_LD);
+    float a[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float4 v = row[q];
+        a[4 * q] = v.x;
+        a[4 * q + 1] = v.y;
+        a[4 * q + 2] = v.z;
+        a[4 * q + 3] = v.w;
+    }
+    float sum = -0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        float total = 0.0f;
+        total = total + a[l];
+        total = total + a[l + 8];
+        total = total + a[l + 16];
+        total = total + a[l + 24];
+        sum = sum + total;
+    }
+    const uint32_t e = blockIdx.x * CZ_RT_EXP + el;
+    if (e < E && t < nt) {
+        float lg = sum;
+        if (L.router_bias) lg = lg + L.router_bias[e];
+        A.logits[(uint64_t)(t0 + t) * E + e] = lg;
     }
 }
 

@@ -129,7 +129,9 @@ int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, u
 
 /* Same on device pointers, asynchronous on `stream` (a hipStream_t; NULL =
  * the library's stream).  Pointers must stay valid until the stream
- * reaches the end of this work. */
+ * reaches the end of this work.  Activation buffers (x_dev, out_dev, and
+ * x_dev of the chain and stream entry points below) must be 16-byte
+ * aligned, as hipMalloc returns them; -1 otherwise. */
 int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, int S, float *out_dev, uint32_t *idx_dev,
                                 float *gates_dev, void *stream);
 

@@ -65,6 +65,18 @@ def test_grouped_norm_topk_false_and_ragged(gpu, oracle_lib):
     _check(Lg, Lo, synth.hidden_states(37, 256, seed=5), "S=37")
 
 
+def test_grouped_many_experts_two_rounds(gpu, oracle_lib):
+    """512 experts, top-10, 160 tokens with Zipf(1.1) skew: 1600 slots, more
+    than the dispatch ranks in one round at 512 experts (1024 slots)."""
+    say("grouped 512 experts top-10 S=160")
+    host = synth.make_layer(256, 512, 10, 128, 0, True, seed=88)
+    host["router_bias"] = synth.zipf_router_bias(512, 1.1, seed=88)
+    Lg = moe.register_layer(1700, host)
+    Lo = oracle_lib.OracleLayer(host)
+    err = _check(Lg, Lo, synth.hidden_states(160, 256, seed=88), "E=512 S=160")
+    say(f"  rel L2 {err:.2e}")
+
+
 def test_grouped_deterministic(gpu):
     say("grouped determinism")
     host = synth.make_layer(512, 16, 4, 256, 0, True, seed=9)
