@@ -412,11 +412,26 @@ __device__ __forceinline__ void cz_gg_rescale(float sc, float &cur, cz_float16v 
 // once by their producer) and weights are loaded into registers while this
 // block is multiplied; A goes through LDS (two buffers), weights straight
 // from HBM into the MFMA operands.  Several workgroups per CU hide the latency.
+// MFMA-layout reads of a wave's staged weights (see k_gg).
+__device__ __forceinline__ void cz_gg_read_w(const uint8_t *lw, uint32_t lane, uint4 (&w)[2][4]) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const uint32_t R = 32u * m + (lane & 31u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t c = 4u * (lane >> 5) + q;
+            w[m][q] = *(const uint4 *)(lw + R * CZ_GG_KB + ((c ^ (R & 7u)) << 4));
+        }
+    }
+}
+
 template <int MODE>
-__global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
+__global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem P) {
     constexpr uint32_t NCOL = cz_gg_cols<MODE>();
     // two LDS buffers of the A tile (hi at +0, lo at +CZ_GG_M*256)
     __shared__ __align__(16) uint8_t lds0[2 * CZ_GG_M * 256], lds1[2 * CZ_GG_M * 256];
+    // per wave: its 64 weight rows x 128 bytes of the current K block
+    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_KB];
     __shared__ uint32_t s_rowsrc[CZ_GG_M];  // A row of each tile row (padding: row 0 of the problem)
     __shared__ uint32_t s_rowdst[CZ_GG_M];  // C row of each tile row (~0u = padding)
 
@@ -456,10 +471,10 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
     const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
     const uint8_t *W0 = P.w0 + sl * P.w_stride;
     const float *S0 = P.s0 + sl * P.s_stride;
-    // subtile m of this wave: its 32 columns, this lane's weight row n and K half
+    // subtile m of this wave: its 32 columns (weight rows)
     const uint8_t *wbase[2];
     const float *srow[2];
-    uint32_t ncol[2], woff[2];
+    uint32_t ncol[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
         const uint32_t nb = MODE == GG_GATEUP ? nt * NCOL + wave * 32u : nt * NCOL + wave * 64u + 32u * m;
@@ -467,17 +482,18 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
         const uint64_t moff = (MODE == GG_GATEUP && m) ? P.w1_off : 0;
         const uint64_t soff = (MODE == GG_GATEUP && m) ? P.s1_off : 0;
         wbase[m] = W0 + moff + (uint64_t)nb * P.Kd;                 // wave-uniform
-        woff[m] = (lane & 31u) * P.Kd + (lane >> 5) * 64u;          // per lane
         srow[m] = S0 + soff + (uint64_t)(nb / CZ_BLOCK) * P.nbK;
     }
-    auto load_w = [&](uint32_t kb, uint4 (&w)[2][4]) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const uint4 *p = (const uint4 *)(wbase[m] + (uint64_t)kb * CZ_GG_KB + woff[m]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[m][q] = p[q];
-        }
-    };
+    // Weights of a K block: the wave's 64 rows (row R: subtile R/32, column
+    // R%32) x 128 bytes.  Load p reads rows 8p .. 8p+7 whole (lane l: row 8p +
+    // l/8, 16-byte chunk l%8), so each instruction covers 8 full 128-byte
+    // lines.  In the wave's LDS buffer chunk c of row R sits at chunk c ^ (R %
+    // 8): the MFMA-layout reads (lane L: row 32m + L%32, chunks 4(L/32) .. +3)
+    // of 8 consecutive lanes then fall in distinct banks.
+    uint8_t *lw = ldsw[wave];
+    const uint32_t wl_off = (lane >> 3) * P.Kd + (lane & 7u) * 16u;                   // global, per lane
+    const uint32_t wl_lds = (lane >> 3) * CZ_GG_KB + (((lane & 7u) ^ (lane >> 3)) << 4);  // LDS, + p*1024
+
 
     cz_float16v acc[2];
 #pragma unroll
@@ -487,30 +503,70 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem P) {
     float cur[2] = {0.0f, 0.0f};
 
     const uint32_t nkb = P.Kd / CZ_GG_KB;  // >= 1
-    uint4 w[2][4], wn[2][4];
-    CzA4 an = cz_gg_load_a(P.a_hi, P.a_lo, aoff, 0);
-    load_w(0, w);
-    cz_gg_store_a(lds0, tid, an);
-    __syncthreads();
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        const uint8_t *rd = (kb & 1) ? lds1 : lds0;
-        uint8_t *wr = (kb & 1) ? lds0 : lds1;
-        const float s0 = cz_const_f32(srow[0] + kb), s1 = cz_const_f32(srow[1] + kb);
-        // block kb+1 (the last block requests itself again): A rows and
-        // weights into registers
-        const uint32_t kn = min(kb + 1, nkb - 1);
-        an = cz_gg_load_a(P.a_hi, P.a_lo, aoff, kn);
-        load_w(kn, wn);
-        cz_gg_rescale(s0, cur[0], acc[0], w[0]);
-        cz_gg_rescale(s1, cur[1], acc[1], w[1]);
-        cz_gg_block(rd, rd + CZ_GG_M * 256, w, acc, lane);
-        cz_gg_store_a(wr, tid, an);
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[m][q] = wn[m][q];
-        __syncthreads();  // block kb+1 is in LDS; buffer rd may be overwritten next
+    uint4 w[2][4];
+    // the 8 weight loads of a K block: lane base (subtile p/4) + uniform row
+    // offset 8(p%4) rows + K offset.  Two register sets (X = a, b) of a
+    // block's A chunks and weights: block kb+2 is requested while block kb is
+    // multiplied and block kb+1 waits in the other set.
+    const uint8_t *gl0 = wbase[0] + wl_off, *gl1 = wbase[1] + wl_off;
+    const uint64_t r8 = 8ull * P.Kd;
+    uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
+    CzA4 an_a, an_b;
+#define CZ_GG_LOAD(X, kb_)                                                      \
+    {                                                                           \
+        const uint32_t kc_ = (kb_);                                             \
+        an_##X = cz_gg_load_a(P.a_hi, P.a_lo, aoff, kc_);                       \
+        const uint64_t ko_ = (uint64_t)kc_ * CZ_GG_KB;                          \
+        X##0 = *(const uint4 *)(gl0 + ko_);                                     \
+        X##1 = *(const uint4 *)(gl0 + r8 + ko_);                                \
+        X##2 = *(const uint4 *)(gl0 + 2 * r8 + ko_);                            \
+        X##3 = *(const uint4 *)(gl0 + 3 * r8 + ko_);                            \
+        X##4 = *(const uint4 *)(gl1 + ko_);                                     \
+        X##5 = *(const uint4 *)(gl1 + r8 + ko_);                                \
+        X##6 = *(const uint4 *)(gl1 + 2 * r8 + ko_);                            \
+        X##7 = *(const uint4 *)(gl1 + 3 * r8 + ko_);                            \
     }
+#define CZ_GG_STORE(X, abuf_)                                                   \
+    {                                                                           \
+        cz_gg_store_a((abuf_), tid, an_##X);                                    \
+        uint8_t *d_ = lw + wl_lds;                                              \
+        *(uint4 *)(d_) = X##0;                                                  \
+        *(uint4 *)(d_ + 1 * 8 * CZ_GG_KB) = X##1;                               \
+        *(uint4 *)(d_ + 2 * 8 * CZ_GG_KB) = X##2;                               \
+        *(uint4 *)(d_ + 3 * 8 * CZ_GG_KB) = X##3;                               \
+        *(uint4 *)(d_ + 4 * 8 * CZ_GG_KB) = X##4;                               \
+        *(uint4 *)(d_ + 5 * 8 * CZ_GG_KB) = X##5;                               \
+        *(uint4 *)(d_ + 6 * 8 * CZ_GG_KB) = X##6;                               \
+        *(uint4 *)(d_ + 7 * 8 * CZ_GG_KB) = X##7;                               \
+    }
+    // one K block: request block kb+2 into set NX, multiply block kb (LDS),
+    // then move block kb+1 (set CX) into LDS; past the end the last block is
+    // requested and stored again (never read)
+#define CZ_GG_STEP(kb_, CX, NX)                                                 \
+    {                                                                           \
+        const uint32_t k_ = (kb_);                                              \
+        const uint8_t *rd_ = (k_ & 1) ? lds1 : lds0;                            \
+        uint8_t *wr_ = (k_ & 1) ? lds0 : lds1;                                  \
+        const float s0_ = cz_const_f32(srow[0] + k_), s1_ = cz_const_f32(srow[1] + k_); \
+        CZ_GG_LOAD(NX, min(k_ + 2, nkb - 1))                                    \
+        cz_gg_read_w(lw, lane, w);                                              \
+        cz_gg_rescale(s0_, cur[0], acc[0], w[0]);                               \
+        cz_gg_rescale(s1_, cur[1], acc[1], w[1]);                               \
+        cz_gg_block(rd_, rd_ + CZ_GG_M * 256, w, acc, lane);                    \
+        CZ_GG_STORE(CX, wr_)                                                    \
+        __syncthreads();                                                        \
+    }
+    CZ_GG_LOAD(a, 0)
+    CZ_GG_STORE(a, lds0)  // the wave's own weight buffer: its DS operations stay in program order
+    CZ_GG_LOAD(a, min(1u, nkb - 1))
+    __syncthreads();
+    for (uint32_t kb = 0; kb < nkb; kb += 2) {
+        CZ_GG_STEP(kb, a, b)
+        if (kb + 1 < nkb) CZ_GG_STEP(kb + 1, b, a)
+    }
+#undef CZ_GG_LOAD
+#undef CZ_GG_STORE
+#undef CZ_GG_STEP
     // epilogue: lane holds rows (i/4)*8 + (l/32)*4 + i%4 of its columns
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
