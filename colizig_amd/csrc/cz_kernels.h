@@ -533,7 +533,7 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
 #pragma unroll
         for (int m = 0; m < M; ++m)
             if (!((chosen >> m) & 1u) && v[m] > lb) lb = v[m];
-        const float bv = cz_wave_max_dpp(lb);
+        const float bv = cz_wave_max_nonneg(lb);  // lb: -1 or an exp value (>= +0)
         uint32_t best = 0xffffffffu;
         if (bv > -1.0f) {
 #pragma unroll
