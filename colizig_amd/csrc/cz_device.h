@@ -148,21 +148,18 @@ __device__ inline float cz_wave_max_dpp(float v) {
 
 __device__ inline uint32_t cz_lane() { return threadIdx.x & (CZ_WAVE - 1); }
 
-// Wave max of values that are non-negative floats or the -1.0f sentinel:
-// those order like their bit patterns read as signed integers, so the max is
-// an integer max (no NaN canonicalisation) with each DPP move folded into it.
-// Four butterfly steps inside each 16-lane row, then row_bcast:15 and
-// row_bcast:31 leave the wave's max in lane 63 (the other rows may hold
-// partial or meaningless values), which is returned to every lane.
-__device__ inline float cz_wave_max_nonneg(float f) {
-    int v = __builtin_bit_cast(int, f);
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true));  // row_half_mirror
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true));  // row_mirror
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x142, 0xF, 0xF, true));  // row_bcast:15
-    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x143, 0xF, 0xF, true));  // row_bcast:31
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 63));
+// Wave max of unsigned integers, returned to every lane: four butterfly DPP
+// steps inside each 16-lane row, row_bcast:15 and row_bcast:31 across rows
+// (a missing DPP source reads 0, the identity of an unsigned max, so every
+// step is exact), then lane 63.  Each DPP move folds into the v_max_u32.
+__device__ inline uint32_t cz_wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));  // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));  // row_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x142, 0xF, 0xF, true));  // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x143, 0xF, 0xF, true));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // DPP move of an integer; lanes whose source lane does not exist (or whose

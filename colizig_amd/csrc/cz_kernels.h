@@ -490,7 +490,7 @@ __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
 // bv = -1 (ties to the lowest id; none left -> expert 0); top = sum of the picked v in f64 in pick order; den = norm_topk ?
 // top : sum_e f64(v_e) in expert order; gate_z = f32(f64(v_z) / den).  Lane l
 // holds experts l + 64m for m < M (M = ceil(E/64)); values move between lanes
-// by DPP, readlane and ballot only.  Lane z < K leaves pick z in registers
+// by DPP and readlane only.  Lane z < K leaves pick z in registers
 // (o_pos = z, o_id, o_gate) and writes s_idx[z] / s_gate[z] (LDS), which the
 // block reads after a barrier.  Must be called by a whole wave.
 // ---------------------------------------------------------------------------
@@ -520,32 +520,32 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
                 if (64 * m + l < E) all += (double)cz_readlane(v[m], l);
     }
     const float v0 = cz_readlane(v[0], 0);
-    uint32_t chosen = 0;  // bit m: expert lane + 64m already picked
+    // moe.zig:447-460 as two wave maxima per pick: vk = bits(v) + 1 for an
+    // unchosen expert with a value (v >= +0 orders like its bits; 0 = chosen,
+    // NaN or past E), the largest vk is the largest value; among the experts
+    // holding it the largest 0xffffffff - id is the lowest id: the strict '>'
+    // scan's winner.  All vk 0: none left -> expert 0.
+    uint32_t vk[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+        vk[m] = (lane + 64u * m < E && v[m] == v[m]) ? __builtin_bit_cast(uint32_t, v[m]) + 1u : 0u;
     double top = 0.0;
     float my_v = 0.0f;    // lane z: value of pick z
     uint32_t my_i = 0;    // lane z: id of pick z
     for (uint32_t z = 0; z < K; ++z) {
-        // moe.zig:447-460: the winner is the largest value, lowest id among
-        // equals: the wave max of each lane's best unchosen value, then the
-        // first 64-expert group whose ballot of (v == max) is non-empty,
-        // lowest lane in it (ids of group m all precede those of group m+1).
-        float lb = -1.0f;
+        uint32_t lk = 0;
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-            if (!((chosen >> m) & 1u) && v[m] > lb) lb = v[m];
-        const float bv = cz_wave_max_nonneg(lb);  // lb: -1 or an exp value (>= +0)
-        uint32_t best = 0xffffffffu;
-        if (bv > -1.0f) {
+        for (int m = 0; m < M; ++m) lk = max(lk, vk[m]);
+        const uint32_t bvk = cz_wave_max_u32(lk);  // uniform
+        uint32_t ik = 0;
 #pragma unroll
-            for (int m = M - 1; m >= 0; --m) {
-                const uint64_t hit = __ballot(!((chosen >> m) & 1u) && v[m] == bv);
-                if (hit) best = 64u * m + (uint32_t)__builtin_ctzll(hit);
-            }
-        }
-        const bool none = best == 0xffffffffu;  // none left -> expert 0
-        if (none) best = 0;
-        const float vb = none ? v0 : bv;        // v[best]
-        if ((best & 63u) == lane) chosen |= 1u << (best >> 6);
+        for (int m = 0; m < M; ++m) ik = max(ik, (bvk != 0u && vk[m] == bvk) ? 0xffffffffu - (lane + 64u * m) : 0u);
+        const uint32_t bik = cz_wave_max_u32(ik);  // uniform
+        const bool none = bvk == 0u;
+        const uint32_t best = none ? 0u : 0xffffffffu - bik;
+        const float vb = none ? v0 : __builtin_bit_cast(float, bvk - 1u);  // v[best]
+#pragma unroll
+        for (int m = 0; m < M; ++m) vk[m] = lane + 64u * m == best ? 0u : vk[m];  // the winner is chosen
         top += (double)vb;  // moe.zig:459 in pick order
         if (lane == z) {
             my_v = vb;
