@@ -204,6 +204,26 @@ def test_deterministic(gpu):
     assert np.array_equal(f32_bits(a), f32_bits(b))
 
 
+def test_misaligned_activations_rejected(gpu):
+    """Device activations move as float4: a pointer off 16-byte alignment is
+    refused (-1, with a message) before anything is launched."""
+    say("misaligned activation pointers")
+    host = synth.make_layer(512, 16, 4, 256, 0, True, seed=12)
+    moe.register_layer(650, host)
+    hip = _lib.hip()
+    xb = moe.DeviceBuffer(2 * 512 * 4 + 64)
+    ob = moe.DeviceBuffer(2 * 512 * 4 + 64)
+    assert hip.colizig_hip_moe_forward_dev(650, xb.ptr + 4, 2, ob.ptr, None, None, None) == -1
+    assert "16-byte" in _lib.last_error()
+    assert hip.colizig_hip_moe_forward_dev(650, xb.ptr, 2, ob.ptr + 8, None, None, None) == -1
+    assert hip.colizig_hip_chain_decode(650, 1, xb.ptr + 4, 1, 1e-6, None, None, None, None) == -1
+    assert hip.colizig_hip_chain_graph_create(650, 1, xb.ptr + 4, 1, 1e-6) < 0
+    # aligned: accepted
+    xb.upload(synth.hidden_states(2, 512, seed=12))
+    assert hip.colizig_hip_moe_forward_dev(650, xb.ptr, 2, ob.ptr, None, None, None) == 0
+    assert hip.colizig_hip_sync() == 0
+
+
 # ------------------------------------------------------------- layer chain --
 def _chain_case(oracle_lib, dims, nl, base, seed, S=1, tokens=3):
     H, E, K, I, SI = dims
