@@ -130,8 +130,11 @@ struct StreamPool {
     uint32_t epoch = 0;
     hipStream_t copy = nullptr;
     hipEvent_t ev_idx = nullptr, ev_copy = nullptr;
-    uint32_t *h_idx = nullptr;         // pinned routing read-back
+    uint32_t *h_idx = nullptr;         // pinned routing read-back (host-coherent)
     size_t h_idx_cap = 0;
+    uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
+    uint32_t seq = 0;
+    uint32_t fills_pending = 0;        // fills enqueued on the copy stream since the compute stream last waited
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
              prefetch_wasted = 0, bytes_h2d = 0;
@@ -694,6 +697,7 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (P.w) (void)hipFree(P.w);
     if (P.s) (void)hipFree(P.s);
     if (P.h_idx) (void)hipHostFree(P.h_idx);
+    if (P.h_flag) (void)hipHostFree(P.h_flag);
     if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
     if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
     if (P.copy) (void)hipStreamDestroy(P.copy);
@@ -1358,6 +1362,7 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
                             hipMemcpyHostToDevice, P.copy), -3);
     CZ_CHECK(hipMemcpyAsync(P.s + (uint64_t)i * P.s_slot, L.host_es + (uint64_t)e * P.s_slot,
                             P.s_slot * sizeof(float), hipMemcpyHostToDevice, P.copy), -3);
+    P.fills_pending++;
     P.bytes_h2d += P.w_slot + P.s_slot * sizeof(float);
     P.loads++;
     P.key[i] = pool_key(layer, e);
@@ -1369,9 +1374,13 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
 }
 
 // Makes the experts `sel` of streamed layer `layer` resident (hits touch the
-// LRU, misses are filled on the copy stream), uploads the layer's slot map on
-// the copy stream, and makes the compute stream wait for all of it.
-int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &sel, hipStream_t st) {
+// LRU, misses are filled on the copy stream).  With `Ld` (at most CZ_SEL_ARGS
+// experts, slots and ids below 2^16) their slots go into Ld's argument table and the compute stream
+// waits for the copy stream only if fills are in flight; otherwise the
+// layer's slot map is uploaded on the copy stream and the compute stream waits
+// for all of it.
+int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &sel, hipStream_t st,
+                    LayerDev *Ld = nullptr) {
     StreamPool &P = g.pool;
     P.epoch++;
     for (uint32_t e : sel) {
@@ -1400,13 +1409,22 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
         P.prefetched[i] = 0;
         L.slot_map[e] = (int32_t)i;
     }
-    // the slot map of this layer: only its selected entries matter (others
-    // may be stale and are never read by this layer's kernels)
-    memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
-    CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
-                            hipMemcpyHostToDevice, P.copy), -3);
-    CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
-    CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
+    if (Ld && sel.size() <= CZ_SEL_ARGS && P.nslots <= 0x10000u && L.d.experts <= 0x10000u) {
+        Ld->sel_n = (uint32_t)sel.size();
+        for (size_t k = 0; k < sel.size(); ++k) Ld->sel[k] = sel[k] | ((uint32_t)L.slot_map[sel[k]] << 16);
+    } else {
+        // the slot map of this layer: only its selected entries matter (others
+        // may be stale and are never read by this layer's kernels)
+        memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
+        CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
+                                hipMemcpyHostToDevice, P.copy), -3);
+        P.fills_pending++;
+    }
+    if (P.fills_pending) {  // the compute stream waits for everything enqueued on the copy stream
+        CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
+        CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
+        P.fills_pending = 0;
+    }
     return 0;
 }
 
@@ -1432,8 +1450,13 @@ int ensure_h_idx(int S) {
     if (P.h_idx) (void)hipHostFree(P.h_idx);
     P.h_idx = nullptr;
     P.h_idx_cap = 0;
-    if (hipHostMalloc(&P.h_idx, kmax * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) return -2;
+    if (hipHostMalloc(&P.h_idx, kmax * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess) return -2;
     P.h_idx_cap = kmax;
+    if (!P.h_flag) {
+        if (hipHostMalloc(&P.h_flag, 64, hipHostMallocCoherent) != hipSuccess) return -2;
+        __atomic_store_n(P.h_flag, 0u, __ATOMIC_RELEASE);
+        P.seq = 0;
+    }
     return 0;
 }
 
@@ -1460,6 +1483,17 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     G.tok_order = w.tok_order;
     G.xh = nullptr;  // routing only: the grouped regime below splits x itself
     G.xl = nullptr;
+    // one token: the routing kernel writes the picks into host memory and then
+    // a sequence number; the host waits on that (no copy, no event)
+    const bool direct = S == 1;
+    if (direct) {
+        void *di = nullptr, *df = nullptr;
+        CZ_CHECK(hipHostGetDevicePointer(&di, P.h_idx, 0), -4);
+        CZ_CHECK(hipHostGetDevicePointer(&df, P.h_flag, 0), -4);
+        G.host_idx = (uint32_t *)di;
+        G.host_flag = (uint32_t *)df;
+        G.host_seq = ++P.seq;
+    }
     switch (cz_route_groups(A.L.E)) {
         case 1: launch_route_tokens<1>(G, st); break;
         case 2: launch_route_tokens<2>(G, st); break;
@@ -1468,15 +1502,35 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         default: launch_route_tokens<16>(G, st); break;
     }
     const size_t nk = (size_t)S * L.d.topk;
-    CZ_CHECK(hipMemcpyAsync(P.h_idx, w.idx, nk * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
-    CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
-    // the routing is on the critical path: poll for it rather than block
-    for (;;) {
-        const hipError_t q = hipEventQuery(P.ev_idx);
-        if (q == hipSuccess) break;
-        if (q != hipErrorNotReady) {
-            snprintf(g_err, sizeof g_err, "routing read-back: %s", hipGetErrorString(q));
-            return -5;
+    if (direct) {
+        CZ_CHECK(hipGetLastError(), -4);
+        // the routing is on the critical path: spin on the flag; now and then
+        // check that the stream is still working (a failed kernel never sets it)
+        for (uint32_t n = 1;; ++n) {
+            if (__atomic_load_n(P.h_flag, __ATOMIC_ACQUIRE) == G.host_seq) break;
+            if ((n & 4095u) == 0) {
+                const hipError_t q = hipStreamQuery(st);
+                if (q == hipSuccess && __atomic_load_n(P.h_flag, __ATOMIC_ACQUIRE) != G.host_seq) {
+                    snprintf(g_err, sizeof g_err, "routing read-back: the routing kernel ended without its flag");
+                    return -5;
+                }
+                if (q != hipSuccess && q != hipErrorNotReady) {
+                    snprintf(g_err, sizeof g_err, "routing read-back: %s", hipGetErrorString(q));
+                    return -5;
+                }
+            }
+        }
+    } else {
+        CZ_CHECK(hipMemcpyAsync(P.h_idx, w.idx, nk * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
+        CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
+        // the routing is on the critical path: poll for it rather than block
+        for (;;) {
+            const hipError_t q = hipEventQuery(P.ev_idx);
+            if (q == hipSuccess) break;
+            if (q != hipErrorNotReady) {
+                snprintf(g_err, sizeof g_err, "routing read-back: %s", hipGetErrorString(q));
+                return -5;
+            }
         }
     }
     std::vector<uint32_t> sel;
@@ -1484,12 +1538,14 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         const uint32_t e = std::min(P.h_idx[k], L.d.experts - 1);
         if (std::find(sel.begin(), sel.end(), e) == sel.end()) sel.push_back(e);
     }
-    int rc = stream_resident(L, layer, sel, st);
+    const bool grouped = grouped_ok(L.d, S);
+    StepArgs A2 = A;  // the decode kernels can take the slots in their arguments
+    int rc = stream_resident(L, layer, sel, st, grouped ? nullptr : &A2.L);
     if (rc) return rc;
     L.last_used = sel;
     if (next && next->streamed() && (rc = stream_prefetch(*next, next_layer))) return rc;
-    if (grouped_ok(L.d, S)) return launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st);
-    return launch_step(A, st, kUp | kDown);
+    if (grouped) return launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st);
+    return launch_step(A2, st, kUp | kDown);
 }
 
 }  // namespace

@@ -62,6 +62,11 @@ struct GroupArgs {
     float *os;                 // [S][H]
     const float *xres;         // [S][H] nullable
     float *out;                // [S][H]
+    // S = 1 routing read back by the host without a copy: the picks go to
+    // host_idx (host memory), then host_seq to host_flag (system scope)
+    uint32_t *host_idx;        // nullable
+    uint32_t *host_flag;
+    uint32_t host_seq;
 };
 
 // ---------------------------------------------------------------------------
@@ -111,6 +116,11 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
         rank += (eq < my_e || (eq == my_e && q < lane)) ? 1u : 0u;
     }
     if (lane < L.K) G.tok_order[(uint64_t)t * L.K + rank] = t * L.K + o_pos;
+    if (G.host_idx) {  // one token (one wave): picks to host memory, then the flag
+        if (lane < L.K) G.host_idx[(uint64_t)t * L.K + o_pos] = o_id;
+        __threadfence_system();
+        if (lane == 0) __hip_atomic_store(G.host_flag, G.host_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     if (split) {
         _Float16 *xh = G.xh + (uint64_t)t * L.H, *xl = G.xl + (uint64_t)t * L.H;
         for (uint32_t i0 = 0; i0 < L.H; i0 += 256 * XB) {

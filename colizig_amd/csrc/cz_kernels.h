@@ -24,8 +24,16 @@
 
 #include "cz_device.h"
 
+#define CZ_SEL_ARGS 8  // selected experts whose pool slots can travel in the kernel arguments
+
 struct LayerDev {
     uint32_t H, E, K, I, SI, norm_topk;
+    // a streamed layer's selected experts and their pool slots, sel[i] =
+    // expert | slot << 16 (sel_n > 0: used instead of slot_map, no slot-map
+    // upload).  Kept in the arguments' first 64 bytes, which every kernel
+    // reads at entry.
+    uint32_t sel_n;
+    uint32_t sel[CZ_SEL_ARGS];
     uint32_t nbH, nbI, nbSI;
     const float *router;   // [E][H]
     const uint8_t *ew;     // expert weight slab
@@ -42,9 +50,15 @@ struct LayerDev {
 
 // Slot of expert e in ew/es: e itself for a resident layer, the pool slot for
 // a streamed one (the host makes every selected expert resident before the
-// layer's expert kernels run; a negative entry maps to slot 0 so that a read
-// stays in bounds).
+// layer's expert kernels run; a negative entry, or an expert missing from the
+// argument table, maps to a valid slot so that a read stays in bounds).
 __device__ inline uint64_t cz_slot(const LayerDev &L, uint32_t e) {
+    if (L.sel_n) {  // e is one of the sel_n selected experts (else the first one's slot)
+        uint32_t s = L.sel[0] >> 16;
+#pragma unroll
+        for (uint32_t i = 1; i < CZ_SEL_ARGS; ++i) s = (i < L.sel_n && (L.sel[i] & 0xffffu) == e) ? L.sel[i] >> 16 : s;
+        return s;
+    }
     return L.slot_map ? (uint64_t)max(L.slot_map[e], 0) : (uint64_t)e;
 }
 
