@@ -149,13 +149,7 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
         }
     }
     if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
-        const float *xs = G.xn + (uint64_t)t * L.H;
-        float d = 0.0f;
-        for (uint32_t i = lane; i < L.H; i += 64) {
-            const float prod = xs[i] * L.sh_gate[i];
-            d = d + prod;
-        }
-        d = cz_wave_sum_dpp(d);
+        const float d = cz_sgate_dot(G.xn + (uint64_t)t * L.H, L.sh_gate, L.H, lane);
         if (lane == 0) G.sgate[t] = cz_sigmoid(d);
     }
 }

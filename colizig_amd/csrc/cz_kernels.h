@@ -62,6 +62,31 @@ __device__ inline uint64_t cz_slot(const LayerDev &L, uint32_t e) {
     return L.slot_map ? (uint64_t)max(L.slot_map[e], 0) : (uint64_t)e;
 }
 
+// Shared-expert gate pre-activation x . sh_gate of one token by one wave
+// (moe.zig:475-477): lane l sums x[i] * g[i] for i = l, l + 64, ... in
+// increasing order (terms past H are not added), then the DPP wave sum.  The
+// loads of 16 terms per lane are in flight at once.
+__device__ inline float cz_sgate_dot(const float *__restrict__ x, const float *__restrict__ g, uint32_t H,
+                                     uint32_t lane) {
+    float d = 0.0f;
+    for (uint32_t i0 = 0; i0 < H; i0 += 64 * 16) {
+        float xv[16], gv[16];
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q) {
+            const uint32_t i = min(i0 + 64 * q + lane, H - 1);  // clamped: in bounds
+            xv[q] = x[i];
+            gv[q] = g[i];
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q) {
+            const float prod = xv[q] * gv[q];
+            const float dn = d + prod;
+            d = i0 + 64 * q + lane < H ? dn : d;
+        }
+    }
+    return cz_wave_sum_dpp(d);
+}
+
 #define CZ_ROUTER_TT 4    // most tokens per router tile
 #define CZ_MAX_E 1024     // experts supported by the top-k wave
 #define CZ_MAX_K 64
@@ -672,13 +697,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         CZ_UP_LOAD_X(it.tok)
         // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         if (it.tile == 0 && wave == 0) {
-            const float *xs = xn + (uint64_t)it.tok * L.H;
-            float d = 0.0f;
-            for (uint32_t i = lane; i < L.H; i += 64) {
-                const float prod = xs[i] * L.sh_gate[i];
-                d = d + prod;
-            }
-            d = cz_wave_sum_dpp(d);
+            const float d = cz_sgate_dot(xn + (uint64_t)it.tok * L.H, L.sh_gate, L.H, lane);
             if (lane == 0) A.sgate[it.tok] = cz_sigmoid(d);
         }
         CZ_UP_STORE_X()
