@@ -520,9 +520,10 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     P.c_lo = w.hl;
     P.routed = 1;
     constexpr uint32_t cu = cz_gg_cols<GG_GATEUP>(), cd = cz_gg_cols<GG_DOWN>();
-    k_gg<GG_GATEUP><<<gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P);
+    // the shared expert's items run in the same launches as the routed ones
+    GGProblem Q{};
     if (L.SI) {
-        GGProblem Q = P;
+        Q = P;
         Q.w0 = L.sw;
         Q.s0 = L.ss;
         Q.w_stride = 0;
@@ -534,8 +535,9 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.c_lo = w.hsl;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
-        k_gg<GG_GATEUP><<<gg_blocks(mts, L.SI, cu), 256, 0, st>>>(G, Q);
     }
+    const uint32_t qu = L.SI ? (mts * (L.SI / cu) + 7) / 8 * 8 : 0u;
+    k_gg<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
     // down
     GGProblem D{};
     D.w0 = L.ew + 2ull * L.I * L.H;
@@ -549,22 +551,23 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     D.a_lo = w.hl;
     D.c = w.o;
     D.routed = 1;
-    k_gg<GG_DOWN><<<gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D);
+    GGProblem QD{};
     if (L.SI) {
-        GGProblem Q = D;
-        Q.w0 = L.sw + 2ull * L.SI * L.H;
-        Q.s0 = L.ss + 2ull * L.nbSI * L.nbH;
-        Q.w_stride = 0;
-        Q.s_stride = 0;
-        Q.Kd = L.SI;
-        Q.nbK = L.nbSI;
-        Q.a_hi = w.hsh;
-        Q.a_lo = w.hsl;
-        Q.c = w.os;
-        Q.routed = 0;
-        Q.rows_total = (uint32_t)S;
-        k_gg<GG_DOWN><<<gg_blocks(mts, L.H, cd), 256, 0, st>>>(G, Q);
+        QD = D;
+        QD.w0 = L.sw + 2ull * L.SI * L.H;
+        QD.s0 = L.ss + 2ull * L.nbSI * L.nbH;
+        QD.w_stride = 0;
+        QD.s_stride = 0;
+        QD.Kd = L.SI;
+        QD.nbK = L.nbSI;
+        QD.a_hi = w.hsh;
+        QD.a_lo = w.hsl;
+        QD.c = w.os;
+        QD.routed = 0;
+        QD.rows_total = (uint32_t)S;
     }
+    const uint32_t qd = L.SI ? (mts * (L.H / cd) + 7) / 8 * 8 : 0u;
+    k_gg<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
     k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

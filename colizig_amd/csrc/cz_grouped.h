@@ -429,9 +429,18 @@ __device__ __forceinline__ void cz_gg_read_w(const uint8_t *lw, uint32_t lane, u
     }
 }
 
+// Work items: the shared expert's (PS, when PS.N != 0) take blocks 0 .. ns-1,
+// so its long items start first and run beside the routed ones; the routed
+// items (PR) take the blocks from ns rounded up to 8, each XCD walking a
+// contiguous range of them.
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem P) {
+__global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem PR, GGProblem PS) {
     constexpr uint32_t NCOL = cz_gg_cols<MODE>();
+    const uint32_t ns = PS.N ? (PS.rows_total + CZ_GG_M - 1) / CZ_GG_M * (PS.N / NCOL) : 0u;
+    const uint32_t ns8 = (ns + 7u) & ~7u;
+    const bool sh = blockIdx.x < ns8;
+    if (sh && blockIdx.x >= ns) return;  // block-uniform
+    const GGProblem P = sh ? PS : PR;
     // two LDS buffers of the A tile (hi at +0, lo at +CZ_GG_M*256)
     __shared__ __align__(16) uint8_t lds0[2 * CZ_GG_M * 256], lds1[2 * CZ_GG_M * 256];
     // per wave: its 64 weight rows x 128 bytes of the current K block
@@ -442,10 +451,15 @@ __global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem P) {
     const uint32_t lane = cz_lane(), tid = threadIdx.x;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
     const uint32_t ntn = P.N / NCOL;
-    const uint32_t mtiles = P.routed ? G.ntiles[0] : (P.rows_total + CZ_GG_M - 1) / CZ_GG_M;
-    const uint32_t T = mtiles * ntn, per = (T + 7) / 8;
-    const uint32_t j = blockIdx.x >> 3, t = (blockIdx.x & 7) * per + j;
-    if (j >= per || t >= T) return;  // block-uniform
+    uint32_t t = blockIdx.x;
+    if (!sh) {
+        const uint32_t b = blockIdx.x - ns8;
+        const uint32_t mtiles = P.routed ? G.ntiles[0] : (P.rows_total + CZ_GG_M - 1) / CZ_GG_M;
+        const uint32_t T = mtiles * ntn, per = (T + 7) / 8;
+        const uint32_t j = b >> 3;
+        t = (b & 7) * per + j;
+        if (j >= per || t >= T) return;  // block-uniform
+    }
     const uint32_t mt = t / ntn, nt = t - mt * ntn;
     uint32_t e = 0, row0, rows;
     if (P.routed) {
