@@ -246,39 +246,37 @@ __device__ inline void cz_router_stage_x(const StepArgs &A, float *smem, uint32_
     }
 }
 
-// Fast-path staging: NX = H/64 input values per lane, all loaded before the
-// sum of squares is formed, so the RMS costs one L2 round trip per token.
+// Fast-path staging of one token row whose NX = H/64 values per lane
+// (columns lane + 64i) are in registers: optional RMS normalisation (the sum
+// of squares in that order, then the DPP wave sum), the row into LDS slot t,
+// and block 0's copy of the normalised row to xn (and xn_trace).
 template <int NX>
-__device__ inline void cz_router_stage_x_reg(const StepArgs &A, float *smem, uint32_t t0, uint32_t nt) {
+__device__ __forceinline__ void cz_router_stage_row(const StepArgs &A, float *smem, uint32_t t0, uint32_t t,
+                                                    float (&xv)[NX]) {
     constexpr uint32_t H = 64 * NX;
     const uint32_t lane = threadIdx.x;
-    const bool pub = A.rms && blockIdx.x == 0;
-    for (uint32_t t = 0; t < nt; ++t) {
-        const float *xs = A.x + (uint64_t)(t0 + t) * H + lane;
-        float xv[NX];
-#pragma unroll
-        for (int i = 0; i < NX; ++i) xv[i] = xs[64 * i];
-        float inv = 1.0f;
-        if (A.rms) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NX; ++i) {
-                const float sq = xv[i] * xv[i];
-                ss = ss + sq;
-            }
-            ss = cz_wave_sum_dpp(ss);
-            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
-        }
-        float *xo = A.xn + (uint64_t)(t0 + t) * H + lane;
-        float *xt = A.xn_trace ? A.xn_trace + (uint64_t)(t0 + t) * H + lane : nullptr;
+    if (A.rms) {
+        float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
-            const float v = A.rms ? xv[i] * inv : xv[i];
-            smem[t * H + lane + 64 * i] = v;
-            if (pub) {
-                xo[64 * i] = v;
-                if (xt) xt[64 * i] = v;
-            }
+            const float sq = xv[i] * xv[i];
+            ss = ss + sq;
+        }
+        ss = cz_wave_sum_dpp(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) xv[i] = xv[i] * inv;
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i) smem[t * H + lane + 64 * i] = xv[i];
+    if (A.rms && blockIdx.x == 0) {  // block-uniform
+        float *xo = A.xn + (uint64_t)(t0 + t) * H + lane;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) xo[64 * i] = xv[i];
+        if (A.xn_trace) {
+            float *xt = A.xn_trace + (uint64_t)(t0 + t) * H + lane;
+#pragma unroll
+            for (int i = 0; i < NX; ++i) xt[64 * i] = xv[i];
         }
     }
 }
@@ -301,13 +299,35 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
     float w[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) w[i] = wr[32 * i];
-    cz_router_stage_x_reg<NS / 2>(A, smem, t0, nt);
+    // the first token's row is requested with the router elements (no wait
+    // between them); later tokens of the tile follow one by one
+    {
+        float xv[NS / 2];
+#pragma unroll
+        for (int i = 0; i < NS / 2; ++i) xv[i] = A.x[(uint64_t)t0 * H + lane + 64 * i];
+        cz_router_stage_row<NS / 2>(A, smem, t0, 0, xv);
+    }
+    for (uint32_t t = 1; t < nt; ++t) {
+        float xv[NS / 2];
+#pragma unroll
+        for (int i = 0; i < NS / 2; ++i) xv[i] = A.x[(uint64_t)(t0 + t) * H + lane + 64 * i];
+        cz_router_stage_row<NS / 2>(A, smem, t0, t, xv);
+    }
     __syncthreads();
+    // the chain's LDS reads go in batches of CB, all in flight before the
+    // batch's FMAs (read one by one, each FMA waited on its read's latency)
+    constexpr int CB = NS < 32 ? NS : 32;
     for (uint32_t t = 0; t < nt; ++t) {
         const float *xs = smem + t * H + j;
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NS; ++i) acc = __builtin_fmaf(xs[32 * i], w[i], acc);
+        for (int i0 = 0; i0 < NS; i0 += CB) {
+            float xb[CB];
+#pragma unroll
+            for (int q = 0; q < CB; ++q) xb[q] = xs[32 * (i0 + q)];
+#pragma unroll
+            for (int q = 0; q < CB; ++q) acc = __builtin_fmaf(xb[q], w[i0 + q], acc);
+        }
         float lg = cz_router_combine(acc, j, hb);
         if (A.L.router_bias) lg = lg + A.L.router_bias[ec];
         if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
