@@ -33,6 +33,7 @@ typedef float cz_float16v __attribute__((ext_vector_type(16)));
 
 #define CZ_GG_M 32        // rows (slots) per M-tile
 #define CZ_GG_KB 128      // K block (= scale block)
+#define CZ_GG_WLD 144     // LDS bytes per staged weight row (128 + 16: rows r..r+7 start in distinct bank groups)
 
 struct GroupArgs {
     LayerDev L;
@@ -414,18 +415,18 @@ __device__ __forceinline__ void cz_gg_rescale(float sc, float &cur, cz_float16v 
 // / 8) + b / 8, so each XCD walks a contiguous range of items and an M-tile's
 // A rows are reused from its L2.  The next K block's A rows (f16 hi/lo, split
 // once by their producer) and weights are loaded into registers while this
-// block is multiplied; A goes through LDS (two buffers), weights straight
-// from HBM into the MFMA operands.  Several workgroups per CU hide the latency.
-// MFMA-layout reads of a wave's staged weights (see k_gg).
+// block is multiplied, then stored to LDS: A to the workgroup's tile, each
+// wave's weights to its own stage.  Three workgroups per CU (168 VGPRs,
+// 52 KiB of LDS each) hide the latency.
+// MFMA-layout reads of a wave's staged weights: lane L reads the 64 bytes
+// 64(L/32) .. +63 of row 32m + L%32 (rows CZ_GG_WLD bytes apart, so the 8
+// rows one read phase touches start in distinct bank groups).
 __device__ __forceinline__ void cz_gg_read_w(const uint8_t *lw, uint32_t lane, uint4 (&w)[2][4]) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
         const uint32_t R = 32u * m + (lane & 31u);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t c = 4u * (lane >> 5) + q;
-            w[m][q] = *(const uint4 *)(lw + R * CZ_GG_KB + ((c ^ (R & 7u)) << 4));
-        }
+        for (int q = 0; q < 4; ++q) w[m][q] = *(const uint4 *)(lw + R * CZ_GG_WLD + 64u * (lane >> 5) + 16u * q);
     }
 }
 
@@ -434,17 +435,17 @@ __device__ __forceinline__ void cz_gg_read_w(const uint8_t *lw, uint32_t lane, u
 // items (PR) take the blocks from ns rounded up to 8, each XCD walking a
 // contiguous range of them.
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem PR, GGProblem PS) {
+__global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem PR, GGProblem PS) {
     constexpr uint32_t NCOL = cz_gg_cols<MODE>();
     const uint32_t ns = PS.N ? (PS.rows_total + CZ_GG_M - 1) / CZ_GG_M * (PS.N / NCOL) : 0u;
     const uint32_t ns8 = (ns + 7u) & ~7u;
     const bool sh = blockIdx.x < ns8;
     if (sh && blockIdx.x >= ns) return;  // block-uniform
     const GGProblem P = sh ? PS : PR;
-    // two LDS buffers of the A tile (hi at +0, lo at +CZ_GG_M*256)
-    __shared__ __align__(16) uint8_t lds0[2 * CZ_GG_M * 256], lds1[2 * CZ_GG_M * 256];
+    // the A tile of the current K block (hi at +0, lo at +CZ_GG_M*256)
+    __shared__ __align__(16) uint8_t lds0[2 * CZ_GG_M * 256];
     // per wave: its 64 weight rows x 128 bytes of the current K block
-    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_KB];
+    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_WLD];
     __shared__ uint32_t s_rowsrc[CZ_GG_M];  // A row of each tile row (padding: row 0 of the problem)
     __shared__ uint32_t s_rowdst[CZ_GG_M];  // C row of each tile row (~0u = padding)
 
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem PR, GGProb
     // of 8 consecutive lanes then fall in distinct banks.
     uint8_t *lw = ldsw[wave];
     const uint32_t wl_off = (lane >> 3) * P.Kd + (lane & 7u) * 16u;                   // global, per lane
-    const uint32_t wl_lds = (lane >> 3) * CZ_GG_KB + (((lane & 7u) ^ (lane >> 3)) << 4);  // LDS, + p*1024
+    const uint32_t wl_lds = (lane >> 3) * CZ_GG_WLD + (lane & 7u) * 16u;  // LDS, + p*8 rows
 
 
     cz_float16v acc[2];
@@ -523,13 +524,12 @@ __global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem PR, GGProb
     const uint32_t nkb = P.Kd / CZ_GG_KB;  // >= 1
     uint4 w[2][4];
     // the 8 weight loads of a K block: lane base (subtile p/4) + uniform row
-    // offset 8(p%4) rows + K offset.  Two register sets (X = a, b) of a
-    // block's A chunks and weights: block kb+2 is requested while block kb is
-    // multiplied and block kb+1 waits in the other set.
+    // offset 8(p%4) rows + K offset.  One register set (a) of a block's A
+    // chunks and weights: block kb+1 is in flight while block kb multiplies.
     const uint8_t *gl0 = wbase[0] + wl_off, *gl1 = wbase[1] + wl_off;
     const uint64_t r8 = 8ull * P.Kd;
-    uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
-    CzA4 an_a, an_b;
+    uint4 a0, a1, a2, a3, a4, a5, a6, a7;
+    CzA4 an_a;
 #define CZ_GG_LOAD(X, kb_)                                                      \
     {                                                                           \
         const uint32_t kc_ = (kb_);                                             \
@@ -549,42 +549,37 @@ __global__ __launch_bounds__(256, 2) void k_gg(GroupArgs G, GGProblem PR, GGProb
         cz_gg_store_a((abuf_), tid, an_##X);                                    \
         uint8_t *d_ = lw + wl_lds;                                              \
         *(uint4 *)(d_) = X##0;                                                  \
-        *(uint4 *)(d_ + 1 * 8 * CZ_GG_KB) = X##1;                               \
-        *(uint4 *)(d_ + 2 * 8 * CZ_GG_KB) = X##2;                               \
-        *(uint4 *)(d_ + 3 * 8 * CZ_GG_KB) = X##3;                               \
-        *(uint4 *)(d_ + 4 * 8 * CZ_GG_KB) = X##4;                               \
-        *(uint4 *)(d_ + 5 * 8 * CZ_GG_KB) = X##5;                               \
-        *(uint4 *)(d_ + 6 * 8 * CZ_GG_KB) = X##6;                               \
-        *(uint4 *)(d_ + 7 * 8 * CZ_GG_KB) = X##7;                               \
+        *(uint4 *)(d_ + 1 * 8 * CZ_GG_WLD) = X##1;                               \
+        *(uint4 *)(d_ + 2 * 8 * CZ_GG_WLD) = X##2;                               \
+        *(uint4 *)(d_ + 3 * 8 * CZ_GG_WLD) = X##3;                               \
+        *(uint4 *)(d_ + 4 * 8 * CZ_GG_WLD) = X##4;                               \
+        *(uint4 *)(d_ + 5 * 8 * CZ_GG_WLD) = X##5;                               \
+        *(uint4 *)(d_ + 6 * 8 * CZ_GG_WLD) = X##6;                               \
+        *(uint4 *)(d_ + 7 * 8 * CZ_GG_WLD) = X##7;                               \
     }
-    // one K block: request block kb+2 into set NX, multiply block kb (LDS),
-    // then move block kb+1 (set CX) into LDS; past the end the last block is
-    // requested and stored again (never read)
-#define CZ_GG_STEP(kb_, CX, NX)                                                 \
-    {                                                                           \
-        const uint32_t k_ = (kb_);                                              \
-        const uint8_t *rd_ = (k_ & 1) ? lds1 : lds0;                            \
-        uint8_t *wr_ = (k_ & 1) ? lds0 : lds1;                                  \
-        const float s0_ = cz_const_f32(srow[0] + k_), s1_ = cz_const_f32(srow[1] + k_); \
-        CZ_GG_LOAD(NX, min(k_ + 2, nkb - 1))                                    \
-        cz_gg_read_w(lw, lane, w);                                              \
-        cz_gg_rescale(s0_, cur[0], acc[0], w[0]);                               \
-        cz_gg_rescale(s1_, cur[1], acc[1], w[1]);                               \
-        cz_gg_block(rd_, rd_ + CZ_GG_M * 256, w, acc, lane);                    \
-        CZ_GG_STORE(CX, wr_)                                                    \
-        __syncthreads();                                                        \
-    }
+    // one K block: multiply block kb (A from LDS, the wave's weights from its
+    // LDS stage), then, once every wave is done with the A tile, move block
+    // kb+1 (loaded during this block) into LDS and request block kb+2 (past
+    // the end the last block is requested again, never stored)
     CZ_GG_LOAD(a, 0)
     CZ_GG_STORE(a, lds0)  // the wave's own weight buffer: its DS operations stay in program order
     CZ_GG_LOAD(a, min(1u, nkb - 1))
     __syncthreads();
-    for (uint32_t kb = 0; kb < nkb; kb += 2) {
-        CZ_GG_STEP(kb, a, b)
-        if (kb + 1 < nkb) CZ_GG_STEP(kb + 1, b, a)
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        const float s0_ = cz_const_f32(srow[0] + kb), s1_ = cz_const_f32(srow[1] + kb);
+        cz_gg_read_w(lw, lane, w);
+        cz_gg_rescale(s0_, cur[0], acc[0], w[0]);
+        cz_gg_rescale(s1_, cur[1], acc[1], w[1]);
+        cz_gg_block(lds0, lds0 + CZ_GG_M * 256, w, acc, lane);
+        if (kb + 1 < nkb) {  // block-uniform
+            __syncthreads();
+            CZ_GG_STORE(a, lds0)
+            CZ_GG_LOAD(a, min(kb + 2, nkb - 1))
+            __syncthreads();
+        }
     }
 #undef CZ_GG_LOAD
 #undef CZ_GG_STORE
-#undef CZ_GG_STEP
     // epilogue: lane holds rows (i/4)*8 + (l/32)*4 + i%4 of its columns
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
