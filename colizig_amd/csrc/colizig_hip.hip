@@ -307,7 +307,15 @@ void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
     if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
         if (A.rms) k_rms_rows<<<(A.S + 3) / 4, 256, 0, st>>>(A);
-        k_router_tiled<<<dim3((L.E + CZ_RT_EXP - 1) / CZ_RT_EXP, (A.S + CZ_RT_TOK - 1) / CZ_RT_TOK), 256 * CZ_RT_TG, 0, st>>>(A);
+        // tokens per workgroup: the most that still gives 256 workgroups
+        const uint32_t ge = (L.E + CZ_RT_EXP - 1) / CZ_RT_EXP;
+        const uint32_t S = (uint32_t)A.S;
+        if (ge * ((S + 15) / 16) >= 256)
+            k_router_tiled<16><<<dim3(ge, (S + 15) / 16), 256 * CZ_RT_TG, 0, st>>>(A);
+        else if (ge * ((S + 7) / 8) >= 256)
+            k_router_tiled<8><<<dim3(ge, (S + 7) / 8), 256 * CZ_RT_TG, 0, st>>>(A);
+        else
+            k_router_tiled<4><<<dim3(ge, (S + 3) / 4), 256 * CZ_RT_TG, 0, st>>>(A);
         return;
     }
     const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);

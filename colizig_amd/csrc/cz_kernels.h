@@ -409,7 +409,8 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
 }
 
 // Many-token router (S > 1): a workgroup of CZ_RT_TG x 256 threads computes
-// CZ_RT_EXP experts x CZ_RT_TOK tokens.  Thread (token group g, half-wave hw
+// CZ_RT_EXP experts x TOK tokens (TOK = 16, 8 or 4: fewer tokens per
+// workgroup for small batches, so the grid still covers the CUs).  Thread (token group g, half-wave hw
 // of its 256, lane j) owns experts 2hw, 2hw + 1 of the tile and tokens
 // [g*NTT, (g+1)*NTT); lane j is chain j: it accumulates columns j, j + 32, ...
 // in increasing order, exactly as the one-token kernel, so logits are
@@ -420,21 +421,21 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
 // combine (cz_router_combine's additions, same order) reads the 32 chain sums
 // from LDS, one thread per logit.  Input: xn when rms = 1 (k_rms_rows ran
 // first), else x.  H % 256 == 0.
-#define CZ_RT_TOK 16
 #define CZ_RT_EXP 16
 #define CZ_RT_TG 2       // token groups (256 threads each)
 #define CZ_RT_ACC_LD 36  // floats per (expert, token) row of chain sums (16 B aligned, b128 conflict-free)
 #define CZ_RT_RING 4     // register sets of chunk operands in flight
 
+template <int TOK>
 __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
-    constexpr uint32_t NTT = CZ_RT_TOK / CZ_RT_TG;  // tokens per thread
+    constexpr uint32_t NTT = TOK / CZ_RT_TG;  // tokens per thread
     const LayerDev &L = A.L;
     const uint32_t H = L.H, E = L.E;
     const uint32_t tid = threadIdx.x, col = tid & 255, g = tid >> 8, hw = col >> 5, j = col & 31;
     const uint32_t ea = min(blockIdx.x * CZ_RT_EXP + 2 * hw, E - 1), eb = min(blockIdx.x * CZ_RT_EXP + 2 * hw + 1, E - 1);
-    const uint32_t t0 = blockIdx.y * CZ_RT_TOK;
-    const uint32_t nt = min((uint32_t)CZ_RT_TOK, (uint32_t)A.S - t0);
-    constexpr uint32_t XBUF = 2 * CZ_RT_TOK * 256, ACCN = CZ_RT_EXP * CZ_RT_TOK * CZ_RT_ACC_LD;
+    const uint32_t t0 = blockIdx.y * TOK;
+    const uint32_t nt = min((uint32_t)TOK, (uint32_t)A.S - t0);
+    constexpr uint32_t XBUF = 2 * TOK * 256, ACCN = CZ_RT_EXP * TOK * CZ_RT_ACC_LD;
     __shared__ __align__(16) float s_buf[XBUF > ACCN ? XBUF : ACCN];
     const float *src = A.rms ? A.xn : A.x;
     const float *wa = L.router + (uint64_t)ea * H + j, *wb = L.router + (uint64_t)eb * H + j;
@@ -462,7 +463,7 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
         for (uint32_t r = 0; r < CZ_RT_RING; ++r) {
             const uint32_t c = cb + r;
             if (c < nch) {  // uniform
-                float *sx = s_buf + (c & 1) * (CZ_RT_TOK * 256);
+                float *sx = s_buf + (c & 1) * (TOK * 256);
 #pragma unroll
                 for (uint32_t t = 0; t < NTT; ++t) sx[(g * NTT + t) * 256 + col] = xv[r][t];
                 float wc[2][8];
@@ -490,13 +491,13 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
     for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (uint32_t t = 0; t < NTT; ++t)
-            s_buf[((2 * hw + m) * CZ_RT_TOK + g * NTT + t) * CZ_RT_ACC_LD + j] = acc[m][t];
+            s_buf[((2 * hw + m) * TOK + g * NTT + t) * CZ_RT_ACC_LD + j] = acc[m][t];
     __syncthreads();
-    if (tid >= CZ_RT_EXP * CZ_RT_TOK) return;
+    if (tid >= CZ_RT_EXP * TOK) return;
     // thread (expert el = tid / 16, token t = tid % 16): total_l = ((0 + a_l)
     // + a_{l+8}) + a_{l+16}) + a_{l+24}, sum = -0 + total_0 + ... + total_7
-    const uint32_t el = tid >> 4, t = tid & 15;
-    const float4 *row = (const float4 *)(s_buf + (el * CZ_RT_TOK + t) * CZ_RT_ACC_LD);
+    const uint32_t el = tid / TOK, t = tid % TOK;
+    const float4 *row = (const float4 *)(s_buf + (el * TOK + t) * CZ_RT_ACC_LD);
     float a[32];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {

@@ -77,6 +77,19 @@ def test_grouped_many_experts_two_rounds(gpu, oracle_lib):
     say(f"  rel L2 {err:.2e}")
 
 
+@pytest.mark.parametrize("E,S", [(128, 256), (128, 512), (256, 64)])
+def test_grouped_router_tile_sizes(gpu, oracle_lib, E, S):
+    """The many-token router picks 16, 8 or 4 tokens per workgroup from E and
+    S (128 experts x 256 tokens: 8; x 512: 16; 256 experts x 64 tokens: 4);
+    every size gives the decode router's logits, so routing stays bit-exact."""
+    say(f"grouped router tiles E={E} S={S}")
+    host = synth.make_layer(256, E, 8, 128, 0, True, seed=E + S)
+    host["router_bias"] = synth.zipf_router_bias(E, 1.1, seed=E + S)
+    Lg = moe.register_layer(1800 + S + E, host)
+    Lo = oracle_lib.OracleLayer(host)
+    _check(Lg, Lo, synth.hidden_states(S, 256, seed=E + S), f"E={E} S={S}")
+
+
 def test_grouped_deterministic(gpu):
     say("grouped determinism")
     host = synth.make_layer(512, 16, 4, 256, 0, True, seed=9)
