@@ -306,7 +306,19 @@ enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
 void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
     if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
-        if (A.rms) k_rms_rows<<<(A.S + 3) / 4, 256, 0, st>>>(A);
+        if (A.rms) {
+            switch ((L.H / 4 + 255) / 256) {  // 128-bit words per thread
+                case 1: k_rms_rows_wg<1><<<A.S, 256, 0, st>>>(A); break;
+                case 2: k_rms_rows_wg<2><<<A.S, 256, 0, st>>>(A); break;
+                case 3: k_rms_rows_wg<3><<<A.S, 256, 0, st>>>(A); break;
+                case 4: k_rms_rows_wg<4><<<A.S, 256, 0, st>>>(A); break;
+                case 5: k_rms_rows_wg<5><<<A.S, 256, 0, st>>>(A); break;
+                case 6: k_rms_rows_wg<6><<<A.S, 256, 0, st>>>(A); break;
+                case 7: k_rms_rows_wg<7><<<A.S, 256, 0, st>>>(A); break;
+                case 8: k_rms_rows_wg<8><<<A.S, 256, 0, st>>>(A); break;
+                default: k_rms_rows<<<(A.S + 3) / 4, 256, 0, st>>>(A); break;
+            }
+        }
         // tokens per workgroup: the most that still gives 256 workgroups
         const uint32_t ge = (L.E + CZ_RT_EXP - 1) / CZ_RT_EXP;
         const uint32_t S = (uint32_t)A.S;

@@ -354,6 +354,59 @@ __device__ __forceinline__ void cz_rms_store(const StepArgs &A, uint64_t o, floa
     }
 }
 
+// One workgroup of 256 threads per token row (H % 256 == 0, H <= 1024 Q):
+// the row is requested at once as 128-bit loads (Q per thread) and staged in
+// LDS; wave 0 forms the sum of squares in the order above, every thread then
+// writes its 4-column groups of xn (and xn_trace) and of the f16 split.
+template <int Q>
+__global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
+    __shared__ __align__(16) float s_row[Q * 1024];
+    __shared__ float s_inv;
+    const uint32_t H = A.L.H, n4 = H / 4, tid = threadIdx.x;
+    const uint64_t row = (uint64_t)blockIdx.x * H;
+    const float4 *x4 = reinterpret_cast<const float4 *>(A.x + row);
+    float4 v[Q];
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k) v[k] = x4[min(tid + 256 * k, n4 - 1)];  // clamped: in bounds
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k)
+        if (tid + 256 * k < n4) reinterpret_cast<float4 *>(s_row)[tid + 256 * k] = v[k];
+    __syncthreads();
+    if (tid < 64) {
+        const uint32_t nq = H / 64;
+        float a[16 * Q];
+#pragma unroll
+        for (uint32_t i = 0; i < 16 * Q; ++i) a[i] = s_row[tid + 64 * min(i, nq - 1)];
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 16 * Q; ++i) {
+            const float sq = i < nq ? a[i] * a[i] : 0.0f;  // past H: + 0, exact
+            ss = ss + sq;
+        }
+        ss = cz_wave_sum_dpp(ss);
+        if (tid == 0) s_inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    typedef _Float16 cz_half4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k) {
+        const uint32_t q = tid + 256 * k;
+        if (q >= n4) break;
+        const float4 y = make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv);
+        reinterpret_cast<float4 *>(A.xn + row)[q] = y;
+        if (A.xn_trace) reinterpret_cast<float4 *>(A.xn_trace + row)[q] = y;
+        if (A.xh) {
+            const cz_half4 hi = {(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+            const cz_half4 lo = {(_Float16)(y.x - (float)hi[0]), (_Float16)(y.y - (float)hi[1]),
+                                 (_Float16)(y.z - (float)hi[2]), (_Float16)(y.w - (float)hi[3])};
+            reinterpret_cast<cz_half4 *>(A.xh + row)[q] = hi;
+            reinterpret_cast<cz_half4 *>(A.xl + row)[q] = lo;
+        }
+    }
+}
+
+// Rows longer than the workgroup form holds: one wave per token.
 __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
     const uint32_t H = A.L.H;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
