@@ -303,6 +303,13 @@ constexpr int kDownKC = 8;    // experts per load batch of the down kernel
 
 enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
 
+// The RMS rows kernel that launch_router runs for these arguments also forms
+// the shared-expert gate (the workgroup-per-row form, with a shared expert).
+bool rms_rows_write_sgate(const StepArgs &A) {
+    const LayerDev &L = A.L;
+    return A.rms && A.S >= kGroupedMinTokens && L.H % 256 == 0 && L.SI != 0 && (L.H / 4 + 255) / 256 <= 8;
+}
+
 void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
     if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
@@ -493,6 +500,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.idx = w.idx;
     G.gates = w.gates;
     G.sgate = w.sgate;
+    G.sgate_ready = rms_rows_write_sgate(A) ? 1u : 0u;
     G.idx_trace = idx_trace;
     G.gates_trace = gates_trace;
     G.counts = w.counts;
@@ -1503,6 +1511,7 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     G.idx = w.idx;
     G.gates = w.gates;
     G.sgate = w.sgate;
+    G.sgate_ready = rms_rows_write_sgate(A) ? 1u : 0u;
     G.tok_order = w.tok_order;
     G.xh = nullptr;  // routing only: the grouped regime below splits x itself
     G.xl = nullptr;

@@ -68,6 +68,7 @@ struct GroupArgs {
     uint32_t *host_idx;        // nullable
     uint32_t *host_flag;
     uint32_t host_seq;
+    uint32_t sgate_ready;      // 1: the RMS rows kernel already wrote sgate
 };
 
 // ---------------------------------------------------------------------------
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
             }
         }
     }
-    if (L.SI != 0) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
+    if (L.SI != 0 && !G.sgate_ready) {  // shared-expert gate sigmoid(x . sh_gate) (moe.zig:475-477)
         const float d = cz_sgate_dot(G.xn + (uint64_t)t * L.H, L.sh_gate, L.H, lane);
         if (lane == 0) G.sgate[t] = cz_sigmoid(d);
     }

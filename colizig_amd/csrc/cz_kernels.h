@@ -357,14 +357,23 @@ __device__ __forceinline__ void cz_rms_store(const StepArgs &A, uint64_t o, floa
 // One workgroup of 256 threads per token row (H % 256 == 0, H <= 1024 Q):
 // the row is requested at once as 128-bit loads (Q per thread) and staged in
 // LDS; wave 0 forms the sum of squares in the order above, every thread then
-// writes its 4-column groups of xn (and xn_trace) and of the f16 split.
+// writes its 4-column groups of xn (and xn_trace) and of the f16 split.  With
+// a shared expert, wave 1 also forms its gate sigmoid(xn . sh_gate) in
+// cz_sgate_dot's order (lane l: columns l, l + 64, ... increasing, then the
+// DPP wave sum), its sh_gate elements requested with the row.
 template <int Q>
 __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
     __shared__ __align__(16) float s_row[Q * 1024];
     __shared__ float s_inv;
-    const uint32_t H = A.L.H, n4 = H / 4, tid = threadIdx.x;
+    const uint32_t H = A.L.H, n4 = H / 4, tid = threadIdx.x, nq = H / 64;
     const uint64_t row = (uint64_t)blockIdx.x * H;
     const float4 *x4 = reinterpret_cast<const float4 *>(A.x + row);
+    const bool gate = A.L.SI != 0 && (tid >> 6) == 1;  // wave-uniform
+    float g[16 * Q];
+    if (gate) {
+#pragma unroll
+        for (uint32_t i = 0; i < 16 * Q; ++i) g[i] = A.L.sh_gate[(tid & 63) + 64 * min(i, nq - 1)];  // clamped
+    }
     float4 v[Q];
 #pragma unroll
     for (uint32_t k = 0; k < Q; ++k) v[k] = x4[min(tid + 256 * k, n4 - 1)];  // clamped: in bounds
@@ -373,7 +382,6 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
         if (tid + 256 * k < n4) reinterpret_cast<float4 *>(s_row)[tid + 256 * k] = v[k];
     __syncthreads();
     if (tid < 64) {
-        const uint32_t nq = H / 64;
         float a[16 * Q];
 #pragma unroll
         for (uint32_t i = 0; i < 16 * Q; ++i) a[i] = s_row[tid + 64 * min(i, nq - 1)];
@@ -388,6 +396,19 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
     }
     __syncthreads();
     const float inv = s_inv;
+    if (gate) {
+        const uint32_t l = tid & 63;
+        float d = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 16 * Q; ++i) {
+            const float y = s_row[l + 64 * min(i, nq - 1)] * inv;  // the xn value of column l + 64i
+            const float prod = y * g[i];
+            const float dn = d + prod;
+            d = i < nq ? dn : d;
+        }
+        d = cz_wave_sum_dpp(d);
+        if (l == 0) A.sgate[blockIdx.x] = cz_sigmoid(d);
+    }
     typedef _Float16 cz_half4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (uint32_t k = 0; k < Q; ++k) {

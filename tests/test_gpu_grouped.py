@@ -142,6 +142,38 @@ def test_grouped_chain_routing(gpu, oracle_lib):
         assert rel_l2(out_g, orcs[l].forward(xn[l])[0]) < RTOL_L2
 
 
+def test_grouped_chain_shared_expert(gpu, oracle_lib):
+    """x <- x + MoE(rms(x)) over 2 layers with a shared expert, S=32 tokens in
+    the grouped regime: the RMS rows kernel also forms the shared-expert gate;
+    the chained result matches the oracle layers applied to the GPU's own
+    router inputs (routing bit-exact, outputs within the bar)."""
+    say("grouped chain with shared expert S=32")
+    H, S, nl = 512, 32, 2
+    hosts = [synth.make_layer(H, 32, 4, 256, 512, True, seed=70 + l) for l in range(nl)]
+    for l, h in enumerate(hosts):
+        moe.register_layer(1900 + l, h)
+    orcs = [oracle_lib.OracleLayer(h) for h in hosts]
+    hip = _lib.hip()
+    x0 = synth.hidden_states(S, H, seed=70)
+    xb = moe.DeviceBuffer(x0.nbytes)
+    xn_t = moe.DeviceBuffer(nl * x0.nbytes)
+    idx_t = moe.DeviceBuffer(nl * S * 4 * 4)
+    xb.upload(x0)
+    assert hip.colizig_hip_chain_decode(1900, nl, xb.ptr, S, 1e-6, xn_t.ptr, idx_t.ptr, None, None) == 0
+    assert hip.colizig_hip_sync() == 0
+    xn = xn_t.download(np.empty((nl, S, H), np.float32))
+    idx = idx_t.download(np.empty((nl, S, 4), np.uint32))
+    x_gpu = xb.download(np.empty((S, H), np.float32))
+    x_ref = x0.astype(np.float64)
+    for l in range(nl):
+        out, ri, _ = orcs[l].forward(xn[l])
+        assert np.array_equal(idx[l], ri), f"layer {l}: routing differs"
+        x_ref = x_ref + out
+    err = rel_l2(x_gpu, x_ref.astype(np.float32))
+    say(f"  rel L2 {err:.2e}")
+    assert err < RTOL_L2
+
+
 def test_prefill_qwen3_30b_shapes_zipf(gpu, oracle_lib):
     """One Qwen3-30B-A3B-shape layer (hidden 2048, 128 experts, top-8, inter
     768) at a 512-token prefill with Zipf(1.1) routing skew, GPU-generated
