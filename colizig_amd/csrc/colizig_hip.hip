@@ -298,7 +298,10 @@ int router_tokens_per_tile(uint32_t H) {
     return (int)std::min<uint32_t>(CZ_ROUTER_TT, std::max<uint32_t>(1u, 8192u / std::max<uint32_t>(H, 1u)));
 }
 
-constexpr int kUpRows = 1;    // rows of each of gate/up per wave
+// rows of each of gate/up per wave: 1, or 2 when that still leaves at least
+// kUpRows2Blocks workgroups (each workgroup stages the token's x once, so two
+// rows per wave halve those reads; with fewer workgroups the grid is too thin)
+constexpr uint32_t kUpRows2Blocks = 1024;
 constexpr int kDownKC = 8;    // experts per load batch of the down kernel
 
 enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
@@ -357,10 +360,17 @@ void launch_up_nm(const StepArgs &A, hipStream_t st) {
         const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + 3) / 4) + (L.SI ? (uint32_t)A.S * ((L.SI + 3) / 4) : 0u);
         k_up_generic<M><<<blocks, 256, 0, st>>>(A);
     } else {
-        const uint32_t rows_wg = 4 * kUpRows;
-        const uint32_t blocks = (uint32_t)A.S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
-                                (L.SI ? (uint32_t)A.S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
-        k_up_fast<NB, kUpRows, M><<<blocks, 256, 0, st>>>(A);
+        auto blocks_for = [&](uint32_t rows_wg) {
+            return (uint32_t)A.S * L.K * ((L.I + rows_wg - 1) / rows_wg) +
+                   (L.SI ? (uint32_t)A.S * ((L.SI + rows_wg - 1) / rows_wg) : 0u);
+        };
+        if constexpr (NB >= 32) {
+            if (blocks_for(8) >= kUpRows2Blocks) {
+                k_up_fast<NB, 2, M><<<blocks_for(8), 256, 0, st>>>(A);
+                return;
+            }
+        }
+        k_up_fast<NB, 1, M><<<blocks_for(4), 256, 0, st>>>(A);
     }
 }
 

@@ -173,6 +173,17 @@ def test_batch_decode(gpu, oracle_lib, S):
     _check_forward(Lg, Lo, synth.hidden_states(S, 512, seed=S), f"S={S}")
 
 
+@pytest.mark.parametrize("S,SI", [(8, 0), (3, 2048)])
+def test_batch_decode_two_rows_per_wave(gpu, oracle_lib, S, SI):
+    """Hidden 2048 with enough gate/up rows that the gate/up kernel takes two
+    rows of each matrix per wave (>= 1024 workgroups of 8 rows)."""
+    say(f"batch decode H=2048 S={S} SI={SI}")
+    host = synth.make_layer(2048, 16, 4, 256, SI, True, seed=40 + S)
+    Lg = moe.register_layer(340 + S, host)
+    Lo = oracle_lib.OracleLayer(host)
+    _check_forward(Lg, Lo, synth.hidden_states(S, 2048, seed=S), f"H=2048 S={S}")
+
+
 @pytest.mark.parametrize("SI,S", [(512, 1), (512, 3), (384, 2)])
 def test_shared_expert(gpu, oracle_lib, SI, S):
     """Qwen4-Exp style: routed experts plus an always-on sigmoid-gated shared
