@@ -422,10 +422,22 @@ bool launch_down_s(const StepArgs &A, hipStream_t st) {
     }
 }
 
-// fast path for I = 256 * {1, 2, 3, 4} and SI = 256 * {0, 1, 2, 4, 8, 16},
-// generic kernel otherwise
+// output rows per wave of the multi-row down kernel
+constexpr int kDownRows = 2;
+
+template <int BPL, int NQ, int KM>
+void launch_down_rows(const StepArgs &A, hipStream_t st) {
+    const uint32_t tiles = (A.L.H + 4 * kDownRows - 1) / (4 * kDownRows);
+    k_down_rows<BPL, NQ, KM, kDownRows><<<(uint32_t)A.S * tiles, 256, 0, st>>>(A);
+}
+
+// multi-row kernel for the Qwen4-Exp shape (I 512, top-10, shared 4096:
+// there the h reads of one row per wave dominate; for the Qwen3-30B-A3B shape
+// one row per wave measured faster); fast path for I = 256 * {1, 2, 3, 4} and
+// SI = 256 * {0, 1, 2, 4, 8, 16}, generic kernel otherwise
 void launch_down(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
+    if (L.I == 512 && L.SI == 4096 && L.K == 10) { launch_down_rows<8, 4, 10>(A, st); return; }
     bool ok = false;
     switch ((L.I % 256) ? 0u : L.I / 256) {
         case 1: ok = launch_down_s<1>(A, st); break;

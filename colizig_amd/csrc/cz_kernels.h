@@ -1044,6 +1044,125 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
     cz_down_row<NJ, NJS, KC>(A, tok, r, lane);
 }
 
+// Down + weighted combine (+ shared expert, + residual), RR output rows per
+// wave: the token's h slices are read into registers once and serve all RR
+// rows, so each row costs only its weight and scale loads.  Lane l owns the
+// routed columns [BPL l, BPL l + BPL) of every expert (I = 64 BPL: one 4, 8,
+// 12 or 16-byte load per expert row) and the shared columns 16l + 1024q (q <
+// NQ = SI/1024: one 16-byte load each).  A dword's columns lie in one
+// 128-column scale block; with BPL = 12 a lane's dwords can span two blocks.
+// KM = top-k (experts in pick order).
+template <int BPL, int NQ, int KM, int RR>
+__global__ __launch_bounds__(256) void k_down_rows(StepArgs A) {
+    constexpr int ND = BPL / 4;
+    static_assert(BPL == 4 || BPL == 8 || BPL == 12 || BPL == 16, "bytes per lane");
+    const LayerDev &L = A.L;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tiles = (L.H + 4 * RR - 1) / (4 * RR);
+    const uint32_t tok = blockIdx.x / tiles, tile = blockIdx.x - tok * tiles;
+    const uint32_t r0 = (tile * 4 + wave) * RR;
+    if (r0 >= L.H || tok >= (uint32_t)A.S) return;  // wave-uniform
+    const uint64_t slot0 = (uint64_t)tok * KM;
+    // the token's h slices (they do not depend on the routing): requested first
+    float hv[KM][BPL];
+#pragma unroll
+    for (int z = 0; z < KM; ++z) {
+        const float4 *hp = reinterpret_cast<const float4 *>(A.h + (slot0 + z) * L.I + BPL * lane);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+            const float4 v = hp[d];
+            hv[z][4 * d] = v.x; hv[z][4 * d + 1] = v.y; hv[z][4 * d + 2] = v.z; hv[z][4 * d + 3] = v.w;
+        }
+    }
+    float hs[NQ > 0 ? NQ : 1][16];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const float4 *hp = reinterpret_cast<const float4 *>(A.hs + (uint64_t)tok * L.SI + 16 * lane + 1024 * q);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const float4 v = hp[d];
+            hs[q][4 * d] = v.x; hs[q][4 * d + 1] = v.y; hs[q][4 * d + 2] = v.z; hs[q][4 * d + 3] = v.w;
+        }
+    }
+    // the routing, wave-uniform: slots, gates
+    uint64_t sl[KM];
+    float gz[KM];
+#pragma unroll
+    for (int z = 0; z < KM; ++z) {
+        const uint32_t e = min(cz_uniform_u32(A.idx + slot0 + z), L.E - 1);
+        gz[z] = cz_uniform_f32(A.gates + slot0 + z);
+        sl[z] = cz_slot(L, e);
+    }
+    const float sgv = NQ > 0 ? cz_uniform_f32(A.sgate + tok) : 0.0f;
+    const uint32_t c0 = BPL * lane, b0 = c0 / CZ_BLOCK, b1 = min((c0 + BPL - 1) / CZ_BLOCK, L.nbI - 1);
+    // every row's weights and scales in flight before any is consumed
+    uint32_t wd[RR][KM][ND];
+    float s0[RR][KM], s1[RR][KM];
+    uint4 ws[RR][NQ > 0 ? NQ : 1];
+    float ssc[RR][NQ > 0 ? NQ : 1];
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) {
+        const uint32_t r = min(r0 + rr, L.H - 1);
+#pragma unroll
+        for (int z = 0; z < KM; ++z) {
+            const uint8_t *wrow = L.ew + sl[z] * L.ew_stride + 2ull * L.I * L.H + (uint64_t)r * L.I + c0;
+            const float *srow = L.es + sl[z] * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbI;
+            if constexpr (ND == 1) {
+                wd[rr][z][0] = *reinterpret_cast<const uint32_t *>(wrow);
+            } else if constexpr (ND == 2) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(wrow);
+                wd[rr][z][0] = v.x; wd[rr][z][1] = v.y;
+            } else if constexpr (ND == 3) {
+                const uint3 v = *reinterpret_cast<const uint3 *>(wrow);
+                wd[rr][z][0] = v.x; wd[rr][z][1] = v.y; wd[rr][z][2] = v.z;
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4 *>(wrow);
+                wd[rr][z][0] = v.x; wd[rr][z][1] = v.y; wd[rr][z][2] = v.z; wd[rr][z][3] = v.w;
+            }
+            s0[rr][z] = srow[b0];
+            s1[rr][z] = BPL == 12 ? srow[b1] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            ws[rr][q] = *reinterpret_cast<const uint4 *>(L.sw + 2ull * L.SI * L.H + (uint64_t)r * L.SI + 16 * lane + 1024 * q);
+            ssc[rr][q] = L.ss[2ull * L.nbSI * L.nbH + (uint64_t)(r / CZ_BLOCK) * L.nbSI + lane / 8 + 8 * q];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int z = 0; z < KM; ++z) {
+            float p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                const float sc = (BPL == 12 && (c0 + 4 * d) / CZ_BLOCK != b0) ? s1[rr][z] : s0[rr][z];
+                p = __builtin_fmaf(cz_dot4_raw(wd[rr][z][d], &hv[z][4 * d], 0.0f), sc, p);
+            }
+            acc = __builtin_fmaf(gz[z], p, acc);
+        }
+        if constexpr (NQ > 0) {
+            float ps = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                float p = cz_dot4_raw(ws[rr][q].x, &hs[q][0], 0.0f);
+                p = cz_dot4_raw(ws[rr][q].y, &hs[q][4], p);
+                p = cz_dot4_raw(ws[rr][q].z, &hs[q][8], p);
+                p = cz_dot4_raw(ws[rr][q].w, &hs[q][12], p);
+                ps = __builtin_fmaf(p, ssc[rr][q], ps);
+            }
+            acc = __builtin_fmaf(sgv, ps, acc);
+        }
+        const float tot = cz_wave_sum_dpp(acc);
+        const uint32_t r = r0 + rr;
+        if (lane == 0 && r < L.H) {
+            const uint64_t o = (uint64_t)tok * L.H + r;
+            A.out[o] = (A.xres ? A.xres[o] : 0.0f) + tot;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // generic (any H, I, SI) forms of the two expert kernels: one wave per row,
 // lanes stride single columns.  Used for shapes the fast paths do not cover.
