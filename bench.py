@@ -73,11 +73,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
-    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn"], default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
                          "512 tokens with Zipf(1.1) routing skew (grouped regime); stream: batch-1 decode "
                          "with the expert set in pinned host memory and a 16 GB HBM expert pool; qwen4: "
-                         "Qwen4-Exp-style stack (36 layers, H4096, E512 top-10, shared 4096) at batch 1 and 32")
+                         "Qwen4-Exp-style stack (36 layers, H4096, E512 top-10, shared 4096) at batch 1 and 32; "
+                         "attn: the FP8 attention projections q/k/v/o of 48 Qwen3-30B-A3B layers at batch 1 "
+                         "(keyed device GEMV)")
     ap.add_argument("--pool-gb", type=float, default=16.0, help="stream: HBM expert pool cap (GB)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -98,6 +100,9 @@ def main():
         return
     if args.workload == "qwen4":
         qwen4_bench(args)
+        return
+    if args.workload == "attn":
+        attn_bench(args)
         return
 
     from colizig_amd import _lib, moe
@@ -449,6 +454,72 @@ def qwen4_bench(args) -> None:
                      "frac": out[1]["hbm_frac"], "traffic": None, "scope": "whole step, batch 1"},
     }
     print(json.dumps(line), flush=True)
+
+
+def attn_bench(args) -> None:
+    """The FP8 attention projections of Qwen3-30B-A3B decode at batch 1
+    (attn.zig:206-208 q/k/v, :260 o; shapes attn.zig:55-58: q [4096][2048],
+    k and v [512][2048], o [2048][4096]) for 48 layers through the keyed
+    device GEMV, each matrix resident under its attnKey (attn.zig:47-50).  The
+    192 launches of a token are captured in one graph on a torch stream (used
+    for the stream and the graph only) and replayed; inputs stay in HBM.
+    Synthetic weights: one random block-FP8 matrix per role, uploaded under
+    every layer's key (each key holds its own HBM copy, so every launch reads
+    its own bytes)."""
+    import torch
+    from colizig_amd import _lib, moe, synth
+    name = moe.init()
+    log(f"device: {name}")
+    NL, H, QD, KVD = args.layers, 2048, 32 * 128, 4 * 128
+    shapes = [(QD, H), (KVD, H), (KVD, H), (H, QD)]  # (O, I) of q, k, v, o
+    rng = np.random.default_rng(0)
+    mats = [synth.block_quantize(rng.normal(0, 0.02, size=(O, I)).astype(np.float32)) for (O, I) in shapes]
+    moe.set_vram_budget(8 << 30)
+    for l in range(NL):
+        for role, (w, s) in enumerate(mats):
+            moe.matrix_load(moe.Fp8Matrix.attn_key(l, role), w, s)
+    dev = torch.device("cuda:0")
+    x = torch.randn(QD, device=dev)            # x (first H entries) and the attention output
+    ys = [torch.empty(O, device=dev) for (O, _) in shapes]
+    st = torch.cuda.Stream(device=dev)
+    hs = ctypes.c_void_p(st.cuda_stream)
+
+    def token():
+        for l in range(NL):
+            for role, (O, I) in enumerate(shapes):
+                moe.matmul_fp8_dev(ys[role].data_ptr(), x.data_ptr(), 1, I, O, moe.Fp8Matrix.attn_key(l, role), hs)
+
+    with torch.cuda.stream(st):
+        token()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        token()
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(st):
+        e0.record(st)
+        for _ in range(args.steps):
+            g.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / args.steps
+    per_token = NL * sum(O * I + nblk(O) * nblk(I) * 4 for (O, I) in shapes)
+    gbs = per_token / (us * 1e-6) / 1e9
+    log(f"attn: {NL} layers x q/k/v/o at batch 1: {us:.1f} us per token, {per_token / 1e6:.1f} MB, {gbs:.0f} GB/s")
+    moe.set_vram_budget(0)
+    print(json.dumps({
+        "metric": "FP8 attention projections q/k/v/o at decode (keyed device GEMV), Qwen3-30B-A3B shape, 1 MI355X",
+        "value": round(1e6 / us, 1), "unit": "tok/s (projections only)", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "e4m3-weights/f32-accumulate", "data": "synthetic (seeded N(0,0.02) weights)",
+        "config": {"workload": "qwen3-30b-a3b-attn-proj-decode", "layers": NL, "hidden": H, "q_dim": QD,
+                   "kv_dim": KVD, "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole token, 192 launches"},
+    }))
 
 
 def calibrate_copy(mib: int) -> None:

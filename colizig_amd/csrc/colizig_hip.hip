@@ -36,6 +36,7 @@ struct Slot {
     void *s = nullptr;
     size_t scap = 0;
     uint64_t clock = 0;
+    int I = 0, O = 0;  // the resident matrix's shape
 };
 constexpr size_t kMaxSlots = 4096;
 
@@ -828,6 +829,8 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
             if (hipMemcpyAsync(g.slots[i].s, scales, sb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
             g.uploaded += wb + sb;
             g.slots[i].key = key;
+            g.slots[i].I = I;
+            g.slots[i].O = O;
             g.by_key[key] = i;
             g.slots[i].clock = ++g.lru;
             wdev = g.slots[i].w;
@@ -848,6 +851,93 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
     if (hipMemcpyAsync(g.h_stage, g.d_y, yb, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return -5;
     if (hipStreamSynchronize(g.stream) != hipSuccess) return -5;
     memcpy(y, g.h_stage, yb);
+    return 0;
+}
+
+// Keyed FP8 GEMV on device pointers: the matrix under `key` must be resident
+// in the keyed HBM cache (colizig_hip_matrix_load, or an earlier
+// colizig_cuda_matmul_fp8 with the same key).
+// rows per wave: 2 when that still leaves kGemvRows2Blocks workgroups
+constexpr int kGemvRows2Blocks = 512;
+
+template <int NB>
+void launch_gemv_fp8(float *y, const float *x, const Slot &sl, int S, int O, hipStream_t st) {
+    constexpr int ST = NB >= 32 ? 128 / NB : 4;  // tokens staged per pass: at most 32 KiB of LDS
+    const uint8_t *w = (const uint8_t *)sl.w;
+    const float *s = (const float *)sl.s;
+    if ((O + 7) / 8 >= kGemvRows2Blocks)
+        k_gemv_fp8<NB, ST, 2><<<(O + 7) / 8, 256, 0, st>>>(y, x, w, s, (uint32_t)S, (uint32_t)O);
+    else
+        k_gemv_fp8<NB, ST, 1><<<(O + 3) / 4, 256, 0, st>>>(y, x, w, s, (uint32_t)S, (uint32_t)O);
+}
+
+extern "C" int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || key == 0 || I < 1 || O < 1 || !w || !scales) return -1;
+    if (g.budget == 0) {
+        snprintf(g_err, sizeof g_err, "matrix_load: no HBM cache budget (colizig_cuda_set_vram_budget)");
+        return -8;
+    }
+    const size_t wb = (size_t)O * I, sb = (size_t)nblk((uint32_t)O) * nblk((uint32_t)I) * sizeof(float);
+    const int i = cache_slot_for(key, wb, sb);
+    if (i < 0) {
+        snprintf(g_err, sizeof g_err, "matrix_load: no cache slot for %zu bytes", wb + sb);
+        return -2;
+    }
+    Slot &sl = g.slots[i];
+    if (sl.wcap < wb || sl.scap < sb) {  // the key was resident with a smaller matrix
+        snprintf(g_err, sizeof g_err, "matrix_load: key resident with another shape");
+        return -1;
+    }
+    CZ_CHECK(hipMemcpyAsync(sl.w, w, wb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipMemcpyAsync(sl.s, scales, sb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    g.uploaded += wb + sb;
+    if (sl.key != key) g.misses++;
+    sl.key = key;
+    sl.I = I;
+    sl.O = O;
+    g.by_key[key] = i;
+    sl.clock = ++g.lru;
+    return 0;
+}
+
+extern "C" int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key,
+                                          void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || I < 1 || O < 1 || !y_dev || !x_dev || !dev_aligned(x_dev, y_dev)) return -1;
+    const auto it = g.by_key.find(key);
+    if (key == 0 || it == g.by_key.end()) {
+        snprintf(g_err, sizeof g_err, "matmul_fp8_dev: key %llu not resident", (unsigned long long)key);
+        return -7;
+    }
+    Slot &sl = g.slots[it->second];
+    if (sl.I != I || sl.O != O) {
+        snprintf(g_err, sizeof g_err, "matmul_fp8_dev: key resident as %d x %d, called as %d x %d", sl.O, sl.I, O, I);
+        return -1;
+    }
+    sl.clock = ++g.lru;
+    g.hits++;
+    const hipStream_t st = pick_stream(stream);
+    switch ((I % 64) ? 0 : I / 64) {
+        case 4: launch_gemv_fp8<4>(y_dev, x_dev, sl, S, O, st); break;
+        case 8: launch_gemv_fp8<8>(y_dev, x_dev, sl, S, O, st); break;
+        case 16: launch_gemv_fp8<16>(y_dev, x_dev, sl, S, O, st); break;
+        case 32: launch_gemv_fp8<32>(y_dev, x_dev, sl, S, O, st); break;
+        case 48: launch_gemv_fp8<48>(y_dev, x_dev, sl, S, O, st); break;
+        case 64: launch_gemv_fp8<64>(y_dev, x_dev, sl, S, O, st); break;
+        default:
+            k_gemm_fp8_generic<<<(O + 3) / 4, 256, 0, st>>>(y_dev, x_dev, (const uint8_t *)sl.w, (const float *)sl.s,
+                                                           S, I, O);
+            break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "matmul_fp8_dev launch: %s", hipGetErrorString(e));
+        return -4;
+    }
     return 0;
 }
 

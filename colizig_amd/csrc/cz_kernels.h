@@ -889,6 +889,56 @@ __device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)
 }
 
 // ---------------------------------------------------------------------------
+// Keyed FP8 GEMV on device-resident activations (attention projections and
+// any other Fp8Matrix at decode, fp8.zig:182): y[S][O] = x[S][I] . (e4m3(W) *
+// scale)^T for W [O][I] resident in HBM.  One wave per output row; lane l owns
+// the row bytes [NB l, NB l + NB) (I = 64 NB, 128-bit loads); a wave takes RW
+// consecutive rows, whose weights and scales are requested before the
+// tokens' rows are staged in LDS, ST tokens at a time, then reused for every
+// token.  Rows past O are read as row O - 1 and not stored (every wave
+// reaches every barrier).
+// ---------------------------------------------------------------------------
+template <int NB, int ST, int RW>
+__global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const float *__restrict__ x,
+                                                  const uint8_t *__restrict__ w, const float *__restrict__ scales,
+                                                  uint32_t S, uint32_t O) {
+    constexpr uint32_t I = 64 * NB, I4 = I / 4, NQ = (ST * I4 + 255) / 256;
+    __shared__ float4 xs[ST * I4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r0 = (blockIdx.x * 4 + wave) * RW;  // the wave's RW rows
+    const uint32_t col0 = lane * NB;
+    uint32_t d[RW][NB / 4];
+    RowScales<NB> rs[RW];
+#pragma unroll
+    for (int q = 0; q < RW; ++q) {
+        const uint32_t row = min(r0 + q, O - 1);
+        cz_load_row<NB>(w + (uint64_t)row * I + col0, d[q]);
+        cz_load_scales<NB>(scales + (uint64_t)(row / CZ_BLOCK) * ((I + CZ_BLOCK - 1) / CZ_BLOCK), col0, rs[q]);
+    }
+    for (uint32_t t0 = 0; t0 < S; t0 += ST) {
+        const uint32_t n4 = min((uint32_t)ST, S - t0) * I4;
+        const float4 *src = reinterpret_cast<const float4 *>(x + (uint64_t)t0 * I);
+        float4 v[NQ];
+#pragma unroll
+        for (uint32_t k = 0; k < NQ; ++k) v[k] = src[min(tid + 256 * k, n4 - 1)];  // clamped: in bounds
+#pragma unroll
+        for (uint32_t k = 0; k < NQ; ++k)
+            if (tid + 256 * k < n4) xs[tid + 256 * k] = v[k];
+        __syncthreads();
+        for (uint32_t t = 0; t < n4 / I4; ++t) {
+            float xv[NB];
+            cz_load_x<NB>(reinterpret_cast<const float *>(xs) + t * I + col0, xv);
+#pragma unroll
+            for (int q = 0; q < RW; ++q) {
+                const float acc = cz_wave_sum_dpp(cz_row_dot<NB>(d[q], xv, rs[q]));
+                if (lane == 0 && r0 + q < O) y[(uint64_t)(t0 + t) * O + r0 + q] = acc;
+            }
+        }
+        __syncthreads();  // these tokens' readers are done before the next pass stores
+    }
+}
+
+// ---------------------------------------------------------------------------
 // gate/up + SiLU, fast path: row width H = 64*NB, RW rows per wave; weights,
 // scales and the input slice are all requested before any is consumed.
 // ---------------------------------------------------------------------------

@@ -75,6 +75,21 @@ def matmul_fp8(x: np.ndarray, w: np.ndarray, scales: np.ndarray, S: int, I: int,
     return y
 
 
+def matrix_load(key: int, w: np.ndarray, scales: np.ndarray) -> None:
+    """Puts an FP8 matrix w[O,I] (+ block scales) under `key` in the HBM cache
+    for matmul_fp8_dev (the keyed cache of fp8.zig:182's GPU leg)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    O, I = w.shape
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    assert scales.size == nblk(O) * nblk(I)
+    _check("colizig_hip_matrix_load", _lib.hip().colizig_hip_matrix_load(key, _p(w), _p(scales), I, O))
+
+
+def matmul_fp8_dev(y_ptr: int, x_ptr: int, S: int, I: int, O: int, key: int, stream=None) -> None:
+    """y[S,O] = x[S,I] @ dequant(W_key)^T on device pointers (asynchronous)."""
+    _check("colizig_hip_matmul_fp8_dev", _lib.hip().colizig_hip_matmul_fp8_dev(y_ptr, x_ptr, S, I, O, key, stream))
+
+
 def dequant_fp8(w: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """GPU dequantisation e4m3(w) * scale (fp8.zig:123-130 semantics)."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
@@ -113,6 +128,11 @@ class Fp8Matrix:
     def expert_key(layer: int, expert: int, role: int) -> int:
         """moe.zig:97-99: 1 + ((layer*512 + expert)*4 + role)"""
         return 1 + (layer * 512 + expert) * 4 + role
+
+    @staticmethod
+    def attn_key(layer: int, role: int) -> int:
+        """attn.zig:47-50 attnKey: expert slot 1020 + role (0..3 = q/k/v/o)."""
+        return Fp8Matrix.expert_key(layer, 1020 + role, 0)
 
 
 def dims(hidden: int, experts: int, topk: int, inter: int, shared_inter: int = 0, norm_topk: bool = True) -> Dims:

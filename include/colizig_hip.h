@@ -66,6 +66,20 @@ void colizig_cuda_shutdown(void);
 int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, const float *scales, int S, int I,
                             int O, uint64_t key);
 
+/* Device-resident form of the keyed matmul above for the FP8 attention
+ * projections (src/qwen3moe/attn.zig:206-208 q/k/v, :260 o, keyed by
+ * attnKey, attn.zig:47-50) and any other Fp8Matrix at decode.
+ * colizig_hip_matrix_load puts w/scales under `key` in the same HBM cache
+ * (synchronous upload; the budget of colizig_cuda_set_vram_budget must be
+ * set: -8 otherwise); a later load or host matmul may evict the slot, so
+ * finish device calls that read a slot before loading what may replace it.
+ * colizig_hip_matmul_fp8_dev: y_dev[S,O] = x_dev[S,I] @ (e4m3(w) *
+ * scales)^T with the matrix resident under key, asynchronous on `stream`
+ * (NULL = the library's stream); x_dev, y_dev 16-byte aligned.  -7 key not
+ * resident; -1 bad args or a shape other than the resident one; -4 launch. */
+int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O);
+int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* 2. MoE-level extensions                                                   */
 /* ------------------------------------------------------------------------ */
