@@ -858,7 +858,7 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
 // in the keyed HBM cache (colizig_hip_matrix_load, or an earlier
 // colizig_cuda_matmul_fp8 with the same key).
 // rows per wave: 2 when that still leaves kGemvRows2Blocks workgroups
-constexpr int kGemvRows2Blocks = 512;
+constexpr int kGemvRows2Blocks = 256;
 
 template <int NB>
 void launch_gemv_fp8(float *y, const float *x, const Slot &sl, int S, int O, hipStream_t st) {
