@@ -73,13 +73,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
-    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead"], default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
                          "512 tokens with Zipf(1.1) routing skew (grouped regime); stream: batch-1 decode "
                          "with the expert set in pinned host memory and a 16 GB HBM expert pool; qwen4: "
                          "Qwen4-Exp-style stack (36 layers, H4096, E512 top-10, shared 4096) at batch 1 and 32; "
                          "attn: the FP8 attention projections q/k/v/o of 48 Qwen3-30B-A3B layers at batch 1 "
-                         "(keyed device GEMV)")
+                         "(keyed device GEMV); lmhead: the BF16 lm_head GEMV (151936 x 2048) at batch 1, "
+                         "dotBf16 order")
     ap.add_argument("--pool-gb", type=float, default=16.0, help="stream: HBM expert pool cap (GB)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -103,6 +104,9 @@ def main():
         return
     if args.workload == "attn":
         attn_bench(args)
+        return
+    if args.workload == "lmhead":
+        lmhead_bench(args)
         return
 
     from colizig_amd import _lib, moe
@@ -519,6 +523,50 @@ def attn_bench(args) -> None:
                    "kv_dim": KVD, "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole token, 192 launches"},
+    }))
+
+
+def lmhead_bench(args) -> None:
+    """The BF16 lm_head of Qwen3-30B-A3B at batch 1: vocab 151936 x hidden
+    2048 rows (622 MB) through the keyed device BF16 GEMV, every dot in
+    dotBf16's order (matmul.zig:84-110), input resident in HBM; back-to-back
+    launches between HIP events on the library stream."""
+    from colizig_amd import _lib, moe
+    name = moe.init()
+    log(f"device: {name}")
+    hip = _lib.hip()
+    V, H = 151936, 2048
+    rng = np.random.default_rng(0)
+    w = (rng.normal(0.0, 0.02, size=(V, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    moe.set_vram_budget(4 << 30)
+    key = moe.Fp8Matrix.expert_key(0, 1000, 3)
+    moe.matrix_load_bf16(key, w)
+    del w
+    xb, yb = moe.DeviceBuffer(H * 4), moe.DeviceBuffer(V * 4)
+    xb.upload(rng.normal(size=(1, H)).astype(np.float32))
+    for _ in range(args.warmup):
+        moe.matmul_bf16_dev(yb.ptr, xb.ptr, 1, H, V, key)
+    assert hip.colizig_hip_sync() == 0
+    ev0, ev1 = hip.colizig_hip_event_create(), hip.colizig_hip_event_create()
+    hip.colizig_hip_event_record(ev0, None)
+    for _ in range(args.steps):
+        moe.matmul_bf16_dev(yb.ptr, xb.ptr, 1, H, V, key)
+    hip.colizig_hip_event_record(ev1, None)
+    assert hip.colizig_hip_sync() == 0
+    us = hip.colizig_hip_event_elapsed_ms(ev0, ev1) * 1000.0 / args.steps
+    nbytes = V * H * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"lmhead: {V} x {H} BF16 at batch 1: {us:.1f} us per token, {nbytes / 1e6:.1f} MB, {gbs:.0f} GB/s")
+    moe.set_vram_budget(0)
+    print(json.dumps({
+        "metric": "BF16 lm_head GEMV at decode (dotBf16 order), Qwen3-30B-A3B shape, 1 MI355X",
+        "value": round(1e6 / us, 1), "unit": "tok/s (lm_head only)", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16-weights/f32-accumulate", "data": "synthetic (seeded N(0,0.02) weights)",
+        "config": {"workload": "qwen3-30b-a3b-lm-head-decode", "vocab": V, "hidden": H, "global_batch": 1,
+                   "seq_len": 1, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "one launch"},
     }))
 
 

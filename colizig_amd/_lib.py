@@ -48,6 +48,8 @@ SIGNATURES = {
                                                ctypes.c_uint64]),
     "colizig_hip_matrix_load": (ctypes.c_int, [ctypes.c_uint64, vp, vp, ctypes.c_int, ctypes.c_int]),
     "colizig_hip_matmul_fp8_dev": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, vp]),
+    "colizig_hip_matrix_load_bf16": (ctypes.c_int, [ctypes.c_uint64, vp, ctypes.c_int, ctypes.c_int]),
+    "colizig_hip_matmul_bf16_dev": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, vp]),
     # extensions
     "colizig_hip_dequant_fp8": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, ctypes.c_int]),
     "colizig_hip_layer_init": (ctypes.c_int, [ctypes.c_uint32, ctypes.POINTER(Dims), vp]),

@@ -37,6 +37,7 @@ struct Slot {
     size_t scap = 0;
     uint64_t clock = 0;
     int I = 0, O = 0;  // the resident matrix's shape
+    int bf16 = 0;      // 1: BF16 rows (no scales), 0: block-FP8
 };
 constexpr size_t kMaxSlots = 4096;
 
@@ -831,6 +832,7 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
             g.slots[i].key = key;
             g.slots[i].I = I;
             g.slots[i].O = O;
+            g.slots[i].bf16 = 0;
             g.by_key[key] = i;
             g.slots[i].clock = ++g.lru;
             wdev = g.slots[i].w;
@@ -898,8 +900,86 @@ extern "C" int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, con
     sl.key = key;
     sl.I = I;
     sl.O = O;
+    sl.bf16 = 0;
     g.by_key[key] = i;
     sl.clock = ++g.lru;
+    return 0;
+}
+
+extern "C" int colizig_hip_matrix_load_bf16(uint64_t key, const uint16_t *w, int I, int O) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || key == 0 || I < 1 || O < 1 || !w) return -1;
+    if (g.budget == 0) {
+        snprintf(g_err, sizeof g_err, "matrix_load_bf16: no HBM cache budget (colizig_cuda_set_vram_budget)");
+        return -8;
+    }
+    const size_t wb = (size_t)O * I * sizeof(uint16_t);
+    const int i = cache_slot_for(key, wb, 16);
+    if (i < 0) {
+        snprintf(g_err, sizeof g_err, "matrix_load_bf16: no cache slot for %zu bytes", wb);
+        return -2;
+    }
+    Slot &sl = g.slots[i];
+    if (sl.wcap < wb) {
+        snprintf(g_err, sizeof g_err, "matrix_load_bf16: key resident with another shape");
+        return -1;
+    }
+    CZ_CHECK(hipMemcpyAsync(sl.w, w, wb, hipMemcpyHostToDevice, g.stream), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    g.uploaded += wb;
+    if (sl.key != key) g.misses++;
+    sl.key = key;
+    sl.I = I;
+    sl.O = O;
+    sl.bf16 = 1;
+    g.by_key[key] = i;
+    sl.clock = ++g.lru;
+    return 0;
+}
+
+template <int NS>
+void launch_gemv_bf16(float *y, const float *x, const Slot &sl, int S, int O, hipStream_t st) {
+    constexpr int WPB = 8;
+    k_gemv_bf16<NS, WPB><<<(O + 2 * WPB - 1) / (2 * WPB), 64 * WPB, 0, st>>>(y, x, (const uint16_t *)sl.w,
+                                                                              (uint32_t)S, (uint32_t)O);
+}
+
+extern "C" int colizig_hip_matmul_bf16_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key,
+                                           void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || I < 1 || O < 1 || !y_dev || !x_dev || !dev_aligned(x_dev, y_dev)) return -1;
+    const auto it = g.by_key.find(key);
+    if (key == 0 || it == g.by_key.end()) {
+        snprintf(g_err, sizeof g_err, "matmul_bf16_dev: key %llu not resident", (unsigned long long)key);
+        return -7;
+    }
+    Slot &sl = g.slots[it->second];
+    if (!sl.bf16 || sl.I != I || sl.O != O) {
+        snprintf(g_err, sizeof g_err, "matmul_bf16_dev: key resident as %s %d x %d, called as BF16 %d x %d",
+                 sl.bf16 ? "BF16" : "FP8", sl.O, sl.I, O, I);
+        return -1;
+    }
+    sl.clock = ++g.lru;
+    g.hits++;
+    const hipStream_t st = pick_stream(stream);
+    switch ((I % 32) ? 0 : I / 32) {
+        case 8: launch_gemv_bf16<8>(y_dev, x_dev, sl, S, O, st); break;
+        case 16: launch_gemv_bf16<16>(y_dev, x_dev, sl, S, O, st); break;
+        case 32: launch_gemv_bf16<32>(y_dev, x_dev, sl, S, O, st); break;
+        case 64: launch_gemv_bf16<64>(y_dev, x_dev, sl, S, O, st); break;
+        case 96: launch_gemv_bf16<96>(y_dev, x_dev, sl, S, O, st); break;
+        case 128: launch_gemv_bf16<128>(y_dev, x_dev, sl, S, O, st); break;
+        default:
+            snprintf(g_err, sizeof g_err, "matmul_bf16_dev: row width %d (supported: 32 x {8,16,32,64,96,128})", I);
+            return -1;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "matmul_bf16_dev launch: %s", hipGetErrorString(e));
+        return -4;
+    }
     return 0;
 }
 
@@ -914,8 +994,9 @@ extern "C" int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int 
         return -7;
     }
     Slot &sl = g.slots[it->second];
-    if (sl.I != I || sl.O != O) {
-        snprintf(g_err, sizeof g_err, "matmul_fp8_dev: key resident as %d x %d, called as %d x %d", sl.O, sl.I, O, I);
+    if (sl.bf16 || sl.I != I || sl.O != O) {
+        snprintf(g_err, sizeof g_err, "matmul_fp8_dev: key resident as %s %d x %d, called as FP8 %d x %d",
+                 sl.bf16 ? "BF16" : "FP8", sl.O, sl.I, O, I);
         return -1;
     }
     sl.clock = ++g.lru;

@@ -939,6 +939,60 @@ __global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const f
 }
 
 // ---------------------------------------------------------------------------
+// BF16 GEMV on device-resident activations (lm_head and other BF16
+// NativeMatrix rows, matmul.zig:84-110 dotBf16): y[S][O] with each dot in
+// dotBf16's order, which is dotF32's (matmul.zig:60-82) on the widened
+// weights: half-wave per row as the router kernel (lane j = chain j over
+// elements j + 32i, then cz_router_combine), so results are bit-identical to
+// the reference's.  WPB waves per workgroup (2 WPB rows) share the token rows
+// staged in LDS, ST at a time; I = 32 NS.  Rows past O are read as row O - 1
+// and not stored (every wave reaches every barrier).
+// ---------------------------------------------------------------------------
+template <int NS, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_gemv_bf16(float *__restrict__ y, const float *__restrict__ x,
+                                                        const uint16_t *__restrict__ w, uint32_t S, uint32_t O) {
+    constexpr uint32_t I = 32 * NS, I4 = I / 4, NT = 64 * WPB;
+    constexpr uint32_t ST = I >= 8192 ? 1 : 8192 / I < 4 ? 8192 / I : 4;  // tokens per pass: <= 32 KiB of LDS
+    constexpr uint32_t NQ = (ST * I4 + NT - 1) / NT;
+    __shared__ float4 xs[ST * I4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
+    const uint32_t r = blockIdx.x * 2 * WPB + 2 * wave + half;
+    const uint32_t row = min(r, O - 1);
+    float wv[NS];
+    const uint16_t *wr = w + (uint64_t)row * I + j;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) wv[i] = __builtin_bit_cast(float, (uint32_t)wr[32 * i] << 16);
+    constexpr int CB = NS < 32 ? NS : 32;
+    for (uint32_t t0 = 0; t0 < S; t0 += ST) {
+        const uint32_t n4 = min(ST, S - t0) * I4;
+        const float4 *src = reinterpret_cast<const float4 *>(x + (uint64_t)t0 * I);
+        float4 v[NQ];
+#pragma unroll
+        for (uint32_t k = 0; k < NQ; ++k) v[k] = src[min(tid + NT * k, n4 - 1)];  // clamped: in bounds
+#pragma unroll
+        for (uint32_t k = 0; k < NQ; ++k)
+            if (tid + NT * k < n4) xs[tid + NT * k] = v[k];
+        __syncthreads();
+        for (uint32_t t = 0; t < n4 / I4; ++t) {
+            const float *xr = reinterpret_cast<const float *>(xs) + t * I + j;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i0 = 0; i0 < NS; i0 += CB) {
+                float xb[CB];
+#pragma unroll
+                for (int q = 0; q < CB; ++q) xb[q] = xr[32 * (i0 + q)];
+#pragma unroll
+                for (int q = 0; q < CB; ++q) acc = __builtin_fmaf(xb[q], wv[i0 + q], acc);
+            }
+            const float lg = cz_router_combine(acc, j, hb);
+            if (j == 0 && r < O) y[(uint64_t)(t0 + t) * O + r] = lg;
+        }
+        __syncthreads();  // these tokens' readers are done before the next pass stores
+    }
+}
+
+// ---------------------------------------------------------------------------
 // gate/up + SiLU, fast path: row width H = 64*NB, RW rows per wave; weights,
 // scales and the input slice are all requested before any is consumed.
 // ---------------------------------------------------------------------------

@@ -90,6 +90,18 @@ def matmul_fp8_dev(y_ptr: int, x_ptr: int, S: int, I: int, O: int, key: int, str
     _check("colizig_hip_matmul_fp8_dev", _lib.hip().colizig_hip_matmul_fp8_dev(y_ptr, x_ptr, S, I, O, key, stream))
 
 
+def matrix_load_bf16(key: int, w_bits: np.ndarray) -> None:
+    """Puts BF16 rows w[O,I] (uint16 bits) under `key` in the HBM cache."""
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    O, I = w_bits.shape
+    _check("colizig_hip_matrix_load_bf16", _lib.hip().colizig_hip_matrix_load_bf16(key, _p(w_bits), I, O))
+
+
+def matmul_bf16_dev(y_ptr: int, x_ptr: int, S: int, I: int, O: int, key: int, stream=None) -> None:
+    """y[S,O] = dotBf16 rows (matmul.zig:84-110) on device pointers (asynchronous)."""
+    _check("colizig_hip_matmul_bf16_dev", _lib.hip().colizig_hip_matmul_bf16_dev(y_ptr, x_ptr, S, I, O, key, stream))
+
+
 def dequant_fp8(w: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """GPU dequantisation e4m3(w) * scale (fp8.zig:123-130 semantics)."""
     w = np.ascontiguousarray(w, dtype=np.uint8)

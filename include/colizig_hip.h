@@ -80,6 +80,16 @@ int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, co
 int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O);
 int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key, void *stream);
 
+/* BF16 rows (lm_head and the other BF16 NativeMatrix GEMVs: dotBf16,
+ * src/ops/matmul.zig:84-110; tensors.zig's NativeMatrix(bf16).matmul) on
+ * device activations: colizig_hip_matrix_load_bf16 puts w [O][I] (BF16 bits)
+ * under `key` in the same HBM cache; colizig_hip_matmul_bf16_dev computes
+ * y_dev[S,O] with every dot in dotBf16's operation order (bit-identical to
+ * the reference), asynchronous on `stream`.  I = 32 * {8,16,32,64,96,128}.
+ * Return codes as for the FP8 pair; a key loaded as the other type is -1. */
+int colizig_hip_matrix_load_bf16(uint64_t key, const uint16_t *w, int I, int O);
+int colizig_hip_matmul_bf16_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* 2. MoE-level extensions                                                   */
 /* ------------------------------------------------------------------------ */

@@ -182,6 +182,21 @@ def matmul_fp8(x, w, s, S, I, O):
     return y
 
 
+def matmul_f32(x, w, S, I, O):
+    """matmul.zig:21-33 with dotF32 (matmul.zig:60-82): y[S,O] = x[S,I] . w[O,I]^T."""
+    y = np.empty((S, O), np.float32)
+    lib().czo_matmul_f32(_p(y), _p(np.ascontiguousarray(x, np.float32)), _p(np.ascontiguousarray(w, np.float32)),
+                         S, I, O)
+    return y
+
+
+def matmul_bf16(x, w_bits, S, I, O):
+    """dotBf16 rows (matmul.zig:84-110): the dotF32 loop with each BF16 weight
+    widened exactly (bits << 16), so it is matmul_f32 on the widened matrix."""
+    w = (np.ascontiguousarray(w_bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return matmul_f32(x, w, S, I, O)
+
+
 def dequant_matrix(w, s):
     w = np.ascontiguousarray(w, np.uint8)
     out = np.empty(w.shape, np.float32)

@@ -149,6 +149,28 @@ def test_dot_order_is_the_reference_lane_order(oracle_lib):
     assert lib.czo_dot_f32(_p(a), _p(b), n) == 0.0
 
 
+def test_matmul_bf16_lane_order_and_widening(oracle_lib):
+    """dotBf16 (matmul.zig:84-110): dotF32's chains with each weight widened
+    as bits << 16.  Planted: x[0] = 1 (acc0 lane 0), x[8] = 2^24 (acc1 lane
+    0), x[16] = -2^24 (acc2 lane 0), x[1] = 1 (acc0 lane 1), weights 1.0 (BF16
+    0x3F80).  Lane 0: (1 + 2^24) rounds to 2^24 (ties to even), - 2^24 = 0;
+    lane 1: 1; the sum is 1.  A left-to-right sum gives 2.  Then random finite
+    BF16 rows against a float64 dot of the widened values."""
+    n = 32
+    x = np.zeros((1, n), np.float32)
+    x[0, 0], x[0, 8], x[0, 16], x[0, 1] = 1.0, 2.0 ** 24, -(2.0 ** 24), 1.0
+    w = np.full((1, n), 0x3F80, np.uint16)
+    assert oracle_lib.matmul_bf16(x, w, 1, n, 1)[0, 0] == 1.0
+    rng = np.random.default_rng(0xBF16)
+    S, I, O = 3, 256, 7
+    bits = (rng.normal(0.0, 0.02, size=(O, I)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    wf = (bits.astype(np.uint32) << 16).view(np.float32)
+    x = rng.normal(size=(S, I)).astype(np.float32)
+    y = oracle_lib.matmul_bf16(x, bits, S, I, O)
+    ref = x.astype(np.float64) @ wf.astype(np.float64).T
+    assert np.all(np.abs(y - ref) <= 1e-5 * np.abs(ref).max() + 1e-30)
+
+
 def test_matmul_fp8_vs_dequant_reference(oracle_lib):
     """fp8.zig:273-311: S=3, I=200, O=5, demo bytes, scales 0.5+U -> 1e-4 abs."""
     rng = np.random.default_rng(0xF8)
