@@ -82,6 +82,9 @@ def main():
                          "(keyed device GEMV); lmhead: the BF16 lm_head GEMV (151936 x 2048) at batch 1, "
                          "dotBf16 order")
     ap.add_argument("--pool-gb", type=float, default=16.0, help="stream: HBM expert pool cap (GB)")
+    ap.add_argument("--priors", action="store_true",
+                    help="stream: warm the pool from learned priors (.colizig_usage written by an untimed "
+                         "previous session of --steps tokens on the same workload) before the timed tokens")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
@@ -358,6 +361,20 @@ def stream_bench(args) -> None:
             set_bias(l)
         return dt
 
+    warmed = None
+    if args.priors:
+        import tempfile
+        from colizig_amd.usage import FILENAME, ExpertUsage
+        for _ in range(steps):  # the previous session, untimed
+            step()
+        with tempfile.TemporaryDirectory() as td:
+            path = os.path.join(td, FILENAME)
+            ExpertUsage.from_pool(0, NL, E).save(path)
+            prior = ExpertUsage.load(path, NL, E)
+        assert prior is not None and hip.colizig_hip_stream_evict_all() == 0
+        warmed = prior.warm_pool(0)
+        log(f"priors: pool warmed with {warmed} experts from {int(prior.counts.sum())} routed counts")
+        c["priors"] = "warm start from .colizig_usage of a previous untimed session of the same length"
     for _ in range(args.warmup):
         step()
     s0 = moe.stream_stats()

@@ -137,6 +137,7 @@ struct StreamPool {
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
     uint32_t seq = 0;
     uint32_t fills_pending = 0;        // fills enqueued on the copy stream since the compute stream last waited
+    std::unordered_map<uint64_t, uint64_t> usage;  // routed-expert counts by pool key (ExpertUsage)
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
              prefetch_wasted = 0, bytes_h2d = 0;
@@ -1608,6 +1609,7 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
     StreamPool &P = g.pool;
     P.epoch++;
     for (uint32_t e : sel) {
+        P.usage[pool_key(layer, e)]++;
         auto it = P.where.find(pool_key(layer, e));
         if (it != P.where.end()) {
             const uint32_t i = it->second;
@@ -1868,6 +1870,78 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
                            : launch_layer(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, st);
         if (rc) return rc;
     }
+    return 0;
+}
+
+// Routed-expert counts of the streamed layers (expert_usage.zig:21-75): one
+// per step in which the expert was selected for the layer.
+extern "C" int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !counts || experts == 0) return -1;
+    const StreamPool &P = g.pool;
+    for (uint32_t l = 0; l < nlayers; ++l)
+        for (uint32_t e = 0; e < experts; ++e) {
+            const auto it = P.usage.find(pool_key(layer0 + l, e));
+            counts[(uint64_t)l * experts + e] = it == P.usage.end() ? 0 : it->second;
+        }
+    return 0;
+}
+
+// Pre-warms the HBM pool from learned priors (warmCaches, expert_usage.zig:
+// 137-160): the streamed (layer, expert) pairs with a non-zero count, hottest
+// first (ties: lower layer, then lower expert), into the pool's free slots
+// only, so a warmed expert never displaces a hotter one.  The pool is one
+// budget across layers, where the reference warms one cache per layer with
+// its top entries.  Fills run on the copy stream and are complete on return;
+// they count as prefetches.  Returns the number of experts warmed.
+extern "C" int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32_t experts, const uint64_t *counts) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    StreamPool &P = g.pool;
+    if (!g.inited || !P.on || !counts || experts == 0) return -1;
+    struct Cand { uint64_t c; uint32_t l, e; };
+    std::vector<Cand> cand;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        if (!L || !L->streamed() || L->d.experts != experts) continue;
+        for (uint32_t e = 0; e < experts; ++e) {
+            const uint64_t c = counts[(uint64_t)l * experts + e];
+            if (c) cand.push_back({c, layer0 + l, e});
+        }
+    }
+    std::stable_sort(cand.begin(), cand.end(), [](const Cand &a, const Cand &b) { return a.c > b.c; });
+    uint32_t next_free = 0, warmed = 0;
+    for (const Cand &k : cand) {
+        if (P.where.count(pool_key(k.l, k.e))) continue;
+        while (next_free < P.nslots && P.key[next_free] != 0) ++next_free;
+        if (next_free == P.nslots) break;
+        const int rc = pool_fill(*find_layer(k.l), k.l, k.e, next_free, true);
+        if (rc) return rc;
+        ++warmed;
+    }
+    CZ_CHECK(hipStreamSynchronize(P.copy), -3);
+    P.fills_pending = 0;
+    return (int)warmed;
+}
+
+// Empties the pool (every slot free; counters and usage kept): the state of a
+// fresh run, for priors measured in the same process.
+extern "C" int colizig_hip_stream_evict_all(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    StreamPool &P = g.pool;
+    if (!g.inited || !P.on) return -1;
+    CZ_CHECK(hipStreamSynchronize(P.copy), -3);
+    CZ_CHECK(hipStreamSynchronize(g.stream), -3);
+    for (uint32_t i = 0; i < P.nslots; ++i) {
+        P.key[i] = 0;
+        P.prefetched[i] = 0;
+    }
+    P.where.clear();
+    P.fills_pending = 0;
+    for (auto &kv : g.layers)
+        if (kv.second.streamed()) std::fill(kv.second.slot_map.begin(), kv.second.slot_map.end(), -1);
     return 0;
 }
 

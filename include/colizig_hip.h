@@ -213,6 +213,20 @@ int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host
  * plain chain, its graph and the read-back hooks refuse them (-1). */
 int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps);
 
+/* Learned priors for the streaming tier (src/runtime/expert_usage.zig:
+ * ExpertUsage counts, :21-75; warmCaches, :137-180).
+ * colizig_hip_stream_usage: counts[l * experts + e] = steps in which layer
+ * layer0 + l routed expert e (since the pool was created).
+ * colizig_hip_stream_warm: fills the pool's free slots with the streamed
+ * (layer, expert) pairs of non-zero count, hottest first (one pool across
+ * layers: the global top, where the reference warms each layer's cache with
+ * its own top); complete on return; returns the number warmed (>= 0).
+ * colizig_hip_stream_evict_all: every slot freed (counters and counts kept).
+ * -1 bad args / no pool; -3 copy error. */
+int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts);
+int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32_t experts, const uint64_t *counts);
+int colizig_hip_stream_evict_all(void);
+
 /* Pool counters, out[0..n): hits, misses, loads, evictions, prefetch_issued,
  * prefetch_hits, prefetch_wasted, bytes_h2d, slots, resident entries. */
 int colizig_hip_stream_stats(uint64_t *out, int n);

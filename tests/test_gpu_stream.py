@@ -101,3 +101,45 @@ def test_stream_refused_by_plain_chain(pool):
     xb.upload(np.zeros((1, H), np.float32))
     assert hip.colizig_hip_chain_decode(2500, 1, xb.ptr, 1, 1e-6, None, None, None, None) == -1
     assert hip.colizig_hip_chain_graph_create(2500, 1, xb.ptr, 1, 1e-6) < 0
+
+
+def test_stream_priors_warm_the_pool(pool):
+    """Learned priors (expert_usage.zig): the pool's routing counts, an empty
+    pool (a fresh run), then a warm start from the counts: the warmed experts
+    are prefetches that later steps hit, and results stay bit-identical to
+    the resident layers."""
+    from colizig_amd.usage import ExpertUsage
+    say("stream priors: count, evict, warm")
+    nl = 2
+    _layers(2300, 2400, nl, seed=57)
+    hip = _lib.hip()
+    x0 = synth.hidden_states(1, H, seed=57)
+    xr, xs = moe.DeviceBuffer(x0.nbytes), moe.DeviceBuffer(x0.nbytes)
+    xr.upload(x0)
+    xs.upload(x0)
+
+    def step(t):
+        assert hip.colizig_hip_chain_decode(2300, nl, xr.ptr, 1, 1e-6, None, None, None, None) == 0
+        assert hip.colizig_hip_stream_decode(2400, nl, xs.ptr, 1, 1e-6) == 0, _lib.last_error()
+        assert hip.colizig_hip_sync() == 0
+        a, b = xr.download(np.empty_like(x0)), xs.download(np.empty_like(x0))
+        assert np.array_equal(f32_bits(a), f32_bits(b)), f"step {t}"
+
+    for t in range(6):
+        step(t)
+    u = ExpertUsage.from_pool(2400, nl, E)
+    assert int(u.counts.sum()) == 6 * nl * K  # one count per selected expert per layer step
+    assert hip.colizig_hip_stream_evict_all() == 0
+    assert moe.stream_stats()["resident"] == 0
+    hot = int((u.counts > 0).sum())
+    st0 = moe.stream_stats()
+    warmed = u.warm_pool(2400)
+    assert warmed == min(NSLOTS, hot)
+    st1 = moe.stream_stats()
+    assert st1["prefetch_issued"] - st0["prefetch_issued"] == warmed
+    assert st1["resident"] == warmed
+    for t in range(6, 9):
+        step(t)
+    st2 = moe.stream_stats()
+    assert st2["prefetch_hits"] > st1["prefetch_hits"]
+    say(f"  warmed {warmed} of {hot}; prefetch hits {st2['prefetch_hits'] - st1['prefetch_hits']}")
