@@ -660,7 +660,7 @@ def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
     t0 = time.time()
     hosts = [orc.OracleLayer(host_layer(hip, L, c)) for L in layers]
     copy_s = time.time() - t0
-    # the GPU box's CPU share is 16 cores per GPU, whatever the affinity mask shows
+    # at most 16 host threads per GPU (the CPU share of a one-GPU host), whatever the affinity mask shows
     threads = min(len(os.sched_getaffinity(0)), 16)
     orc.lib().czo_parallel_enable(threads)
     x = x0.copy()

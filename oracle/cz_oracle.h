@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  This is the oracle the HIP library is checked
  * against; it is never linked into, loaded by or called from the product
  * library.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- * leg use it, and only as the checker / the timed CPU baseline.
+ * leg use it, and only as the reference results / the timed CPU baseline.
  *
  * Every function restates one function of the reference (Zig 0.16 sources,
  * which cannot be compiled here: no zig toolchain) with the same operation

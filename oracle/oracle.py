@@ -1,7 +1,7 @@
 """ctypes wrapper of oracle/libczoracle.so (the C restatement in cz_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP library and the timed CPU
-baseline.  Build with `make -C oracle` (or oracle.oracle.build()).
+TEST INFRASTRUCTURE ONLY: what the HIP library's results are compared against,
+and the timed CPU baseline.  Build with `make -C oracle` (or oracle.oracle.build()).
 """
 from __future__ import annotations
 
