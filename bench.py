@@ -543,6 +543,11 @@ def attn_bench(args) -> None:
     }))
 
 
+# HBM bytes per lm_head launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (303,938 KiB read x 2.0 copy calibration + 594 KiB written)
+LMHEAD_TRAFFIC_BYTES = 303938 * 1024 * 2 + 594 * 1024
+
+
 def lmhead_bench(args) -> None:
     """The BF16 lm_head of Qwen3-30B-A3B at batch 1: vocab 151936 x hidden
     2048 rows (622 MB) through the keyed device BF16 GEMV, every dot in
@@ -583,7 +588,7 @@ def lmhead_bench(args) -> None:
         "config": {"workload": "qwen3-30b-a3b-lm-head-decode", "vocab": V, "hidden": H, "global_batch": 1,
                    "seq_len": 1, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "one launch"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": LMHEAD_TRAFFIC_BYTES, "scope": "one launch"},
     }))
 
 
