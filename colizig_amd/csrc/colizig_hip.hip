@@ -62,6 +62,10 @@ struct LayerHost {
     std::vector<uint8_t> loaded;
     uint32_t nloaded = 0;
     bool shared_set = false;
+    // changes whenever a device buffer the kernels take as an argument is
+    // replaced (re-registration, router bias added or removed, streaming):
+    // a HIP graph captured before then holds stale pointers
+    uint64_t gen = 0;
 
     uint64_t ew_stride() const { return 3ull * d.inter * d.hidden; }
     uint64_t es_stride() const { return 3ull * nblk(d.inter) * nblk(d.hidden); }
@@ -163,6 +167,9 @@ struct Ctx {
     std::vector<void *> retired;
     std::unordered_map<int64_t, hipGraphExec_t> graphs;
     std::unordered_map<int64_t, hipGraph_t> graph_defs;
+    // (layer, generation) of every layer a graph captured
+    std::unordered_map<int64_t, std::vector<std::pair<uint32_t, uint64_t>>> graph_layers;
+    uint64_t layer_gen = 0;
     std::unordered_map<int64_t, hipEvent_t> events;
     int64_t next_handle = 1;
     StreamPool pool;
@@ -817,10 +824,19 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
     if (hipMemcpyAsync(g.d_x, g.h_stage, xb, hipMemcpyHostToDevice, g.stream) != hipSuccess) return -3;
     const void *wdev = nullptr, *sdev = nullptr;
     if (key != 0 && g.budget != 0) {
-        const int i = cache_slot_for(key, wb, sb);
+        int i = cache_slot_for(key, wb, sb);
+        // a hit is used only when the resident matrix is this call's: FP8 rows
+        // of the same shape.  Otherwise the slot is refilled when its buffers
+        // hold this matrix, else the call takes the uncached path.
+        bool same = false;
+        if (i >= 0 && g.slots[i].key == key) {
+            const Slot &sl = g.slots[i];
+            same = sl.bf16 == 0 && sl.I == I && sl.O == O;
+            if (!same && (sl.wcap < wb || sl.scap < sb)) i = -1;
+        }
         if (i < 0) {
-            key = 0;  // cache full of bigger blocks: uncached path
-        } else if (g.slots[i].key == key) {
+            key = 0;  // cache full of bigger blocks, or the key holds another matrix: uncached path
+        } else if (same) {
             g.hits++;
             g.slots[i].clock = ++g.lru;
             wdev = g.slots[i].w;
@@ -1080,6 +1096,7 @@ extern "C" int colizig_hip_layer_init(uint32_t layer, const colizig_dims *dims, 
     if (it != g.layers.end()) free_layer(it->second);
     LayerHost &L = g.layers[layer];
     L.d = d;
+    L.gen = ++g.layer_gen;
     if (hipMalloc(&L.router, (size_t)d.experts * d.hidden * sizeof(float)) != hipSuccess ||
         hipMalloc(&L.ew, L.ew_stride() * d.experts) != hipSuccess ||
         hipMalloc(&L.es, L.es_stride() * d.experts * sizeof(float)) != hipSuccess) {
@@ -1162,13 +1179,19 @@ extern "C" int colizig_hip_layer_set_router_bias(uint32_t layer, const float *bi
     if (!g.inited || !L) return -1;
     (void)hipStreamSynchronize(g.stream);
     if (!bias) {
-        if (L->rbias) (void)hipFree(L->rbias);
+        if (L->rbias) {
+            (void)hipFree(L->rbias);
+            L->gen = ++g.layer_gen;
+        }
         L->rbias = nullptr;
         return 0;
     }
-    if (!L->rbias && hipMalloc(&L->rbias, (size_t)L->d.experts * sizeof(float)) != hipSuccess) {
-        L->rbias = nullptr;
-        return -2;
+    if (!L->rbias) {
+        L->gen = ++g.layer_gen;
+        if (hipMalloc(&L->rbias, (size_t)L->d.experts * sizeof(float)) != hipSuccess) {
+            L->rbias = nullptr;
+            return -2;
+        }
     }
     CZ_CHECK(hipMemcpy(L->rbias, bias, (size_t)L->d.experts * sizeof(float), hipMemcpyHostToDevice), -3);
     return 0;
@@ -1296,6 +1319,8 @@ extern "C" int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlay
     const int64_t h = g.next_handle++;
     g.graphs[h] = exec;
     g.graph_defs[h] = graph;
+    auto &gl = g.graph_layers[h];
+    for (uint32_t l = 0; l < nlayers; ++l) gl.emplace_back(layer0 + l, find_layer(layer0 + l)->gen);
     return h;
 }
 
@@ -1304,6 +1329,16 @@ extern "C" int colizig_hip_graph_launch(int64_t handle, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     auto it = g.graphs.find(handle);
     if (!g.inited || it == g.graphs.end()) return -1;
+    // a layer re-registered (or its router bias or expert source changed)
+    // since the capture: the graph's kernel arguments point at freed buffers
+    for (const auto &lg : g.graph_layers[handle]) {
+        const LayerHost *L = find_layer(lg.first);
+        if (!L || L->gen != lg.second) {
+            snprintf(g_err, sizeof g_err, "graph %lld: layer %u changed since capture; create the graph again",
+                     (long long)handle, lg.first);
+            return -1;
+        }
+    }
     CZ_CHECK(hipGraphLaunch(it->second, pick_stream(stream)), -4);
     return 0;
 }
@@ -1320,6 +1355,7 @@ extern "C" void colizig_hip_graph_destroy(int64_t handle) {
         (void)hipGraphDestroy(jt->second);
         g.graph_defs.erase(jt);
     }
+    g.graph_layers.erase(handle);
 }
 
 // ---- synthetic weights -----------------------------------------------------
@@ -1837,6 +1873,7 @@ extern "C" int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned
     L->host_es = host_es;
     L->ew = P.w;
     L->es = P.s;
+    L->gen = ++g.layer_gen;
     L->slot_map.assign(d.experts, -1);
     if (!L->slot_map_dev && hipMalloc(&L->slot_map_dev, d.experts * sizeof(int32_t)) != hipSuccess) return -2;
     CZ_CHECK(hipMemset(L->slot_map_dev, 0xff, d.experts * sizeof(int32_t)), -4);  // all -1

@@ -148,6 +148,23 @@ __device__ inline float cz_wave_max_dpp(float v) {
 
 __device__ inline uint32_t cz_lane() { return threadIdx.x & (CZ_WAVE - 1); }
 
+// Sum of a double over the 64 lanes (xor butterfly), returned to every lane.
+__device__ inline double cz_wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, CZ_WAVE);
+    return v;
+}
+
+// rmsnorm.zig:32-40 `rms` with a unit weight, from ss = the f64 sum of the
+// row's squares (each f64(v)*v is exact in f64, so the sum differs from the
+// reference's row-order sum only by f64 rounding far below an f32 ulp):
+// mean = f32(ss / n), r = 1 / sqrt(mean + eps) in f32 (correctly rounded
+// division and square root); the row is then x_i * r.
+__device__ inline float cz_rms_inv(double ss, uint32_t n, float eps) {
+    const float mean = (float)(ss / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
 // Wave max of unsigned integers, returned to every lane: four butterfly DPP
 // steps inside each 16-lane row, row_bcast:15 and row_bcast:31 across rows
 // (a missing DPP source reads 0, the identity of an unsigned max, so every

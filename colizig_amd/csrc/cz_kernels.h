@@ -217,22 +217,20 @@ __device__ inline float cz_router_dot(const float *__restrict__ a, const float *
 }
 
 // Router input tile of one block into LDS: tokens t0..t0+nt-1, optionally
-// RMS-normalised (x / sqrt(mean(x^2) + eps)); block 0 of the grid publishes
-// the normalised rows.  blockDim.x == 64 (one wave).
+// RMS-normalised (rmsnorm.zig:32-40 with a unit weight, cz_rms_inv); block 0
+// of the grid publishes the normalised rows.  blockDim.x == 64 (one wave).
 __device__ inline void cz_router_stage_x(const StepArgs &A, float *smem, uint32_t t0, uint32_t nt) {
     const uint32_t H = A.L.H;
     for (uint32_t t = 0; t < nt; ++t) {
         const float *xs = A.x + (uint64_t)(t0 + t) * H;
         float inv = 1.0f;
         if (A.rms) {
-            float ss = 0.0f;
+            double ss = 0.0;
             for (uint32_t i = threadIdx.x; i < H; i += 64) {
-                const float v = xs[i];
-                const float sq = v * v;
-                ss = ss + sq;
+                const double v = (double)xs[i];
+                ss += v * v;
             }
-            ss = cz_wave_sum_dpp(ss);
-            inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+            inv = cz_rms_inv(cz_wave_sum_f64(ss), H, A.eps);
         }
         const bool pub = A.rms && blockIdx.x == 0;
         for (uint32_t i = threadIdx.x; i < H; i += 64) {
@@ -256,14 +254,10 @@ __device__ __forceinline__ void cz_router_stage_row(const StepArgs &A, float *sm
     constexpr uint32_t H = 64 * NX;
     const uint32_t lane = threadIdx.x;
     if (A.rms) {
-        float ss = 0.0f;
+        double ss = 0.0;
 #pragma unroll
-        for (int i = 0; i < NX; ++i) {
-            const float sq = xv[i] * xv[i];
-            ss = ss + sq;
-        }
-        ss = cz_wave_sum_dpp(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        for (int i = 0; i < NX; ++i) ss += (double)xv[i] * (double)xv[i];
+        const float inv = cz_rms_inv(cz_wave_sum_f64(ss), H, A.eps);
 #pragma unroll
         for (int i = 0; i < NX; ++i) xv[i] = xv[i] * inv;
     }
@@ -335,12 +329,11 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
 }
 
 // Many-token router input (S > 1, rms = 1): one wave per token writes xn =
-// x / sqrt(mean(x^2) + eps) in the one-token router's order (lane l sums the
-// squares of columns l, l + 64, ... in increasing order, then the DPP wave
-// sum), and, when xh / xl are given, xn split into f16 hi + lo (the grouped
-// GEMM's A operand).  Rows of up to CZ_RMS_MAXB * 2048 columns stay in
+// rms(x) (rmsnorm.zig:32-40 with a unit weight: the f64 sum of the squares,
+// cz_rms_inv), and, when xh / xl are given, xn split into f16 hi + lo (the
+// grouped GEMM's A operand).  Rows of up to CZ_RMS_MAXB * 2048 columns stay in
 // registers, loaded at once; loads past H read column H - 64 + lane and add
-// +0 (ss >= 0, so ss + 0 = ss exactly).  Longer rows are read twice.
+// +0.  Longer rows are read twice.
 #define CZ_RMS_PB 32   // columns per lane per batch
 #define CZ_RMS_MAXB 2  // register-resident batches
 
@@ -356,7 +349,7 @@ __device__ __forceinline__ void cz_rms_store(const StepArgs &A, uint64_t o, floa
 
 // One workgroup of 256 threads per token row (H % 256 == 0, H <= 1024 Q):
 // the row is requested at once as 128-bit loads (Q per thread) and staged in
-// LDS; wave 0 forms the sum of squares in the order above, every thread then
+// LDS; wave 0 forms the f64 sum of squares (cz_rms_inv), every thread then
 // writes its 4-column groups of xn (and xn_trace) and of the f16 split.  With
 // a shared expert, wave 1 also forms its gate sigmoid(xn . sh_gate) in
 // cz_sgate_dot's order (lane l: columns l, l + 64, ... increasing, then the
@@ -385,14 +378,11 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
         float a[16 * Q];
 #pragma unroll
         for (uint32_t i = 0; i < 16 * Q; ++i) a[i] = s_row[tid + 64 * min(i, nq - 1)];
-        float ss = 0.0f;
+        double ss = 0.0;
 #pragma unroll
-        for (uint32_t i = 0; i < 16 * Q; ++i) {
-            const float sq = i < nq ? a[i] * a[i] : 0.0f;  // past H: + 0, exact
-            ss = ss + sq;
-        }
-        ss = cz_wave_sum_dpp(ss);
-        if (tid == 0) s_inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        for (uint32_t i = 0; i < 16 * Q; ++i) ss += i < nq ? (double)a[i] * (double)a[i] : 0.0;  // past H: + 0
+        ss = cz_wave_sum_f64(ss);
+        if (tid == 0) s_inv = cz_rms_inv(ss, H, A.eps);
     }
     __syncthreads();
     const float inv = s_inv;
@@ -436,7 +426,7 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
     const float *xs = A.x + (uint64_t)t * H;
     const uint64_t row = (uint64_t)t * H;
     const uint32_t nb = (H + 64 * CZ_RMS_PB - 1) / (64 * CZ_RMS_PB);
-    float ss = 0.0f;
+    double ss = 0.0;
     if (nb <= CZ_RMS_MAXB) {
         float v[CZ_RMS_MAXB][CZ_RMS_PB];
 #pragma unroll
@@ -449,13 +439,10 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
         for (uint32_t b = 0; b < CZ_RMS_MAXB; ++b)
             if (b < nb) {
 #pragma unroll
-                for (uint32_t q = 0; q < CZ_RMS_PB; ++q) {
-                    const float sq = 64 * (CZ_RMS_PB * b + q) < H ? v[b][q] * v[b][q] : 0.0f;
-                    ss = ss + sq;
-                }
+                for (uint32_t q = 0; q < CZ_RMS_PB; ++q)
+                    ss += 64 * (CZ_RMS_PB * b + q) < H ? (double)v[b][q] * (double)v[b][q] : 0.0;
             }
-        ss = cz_wave_sum_dpp(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+        const float inv = cz_rms_inv(cz_wave_sum_f64(ss), H, A.eps);
 #pragma unroll
         for (uint32_t b = 0; b < CZ_RMS_MAXB; ++b)
             if (b < nb) {
@@ -472,13 +459,9 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
 #pragma unroll
         for (uint32_t q = 0; q < CZ_RMS_PB; ++q) v[q] = xs[min(i0 + 64 * q, H - 64) + lane];
 #pragma unroll
-        for (uint32_t q = 0; q < CZ_RMS_PB; ++q) {
-            const float sq = i0 + 64 * q < H ? v[q] * v[q] : 0.0f;
-            ss = ss + sq;
-        }
+        for (uint32_t q = 0; q < CZ_RMS_PB; ++q) ss += i0 + 64 * q < H ? (double)v[q] * (double)v[q] : 0.0;
     }
-    ss = cz_wave_sum_dpp(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)H + A.eps);
+    const float inv = cz_rms_inv(cz_wave_sum_f64(ss), H, A.eps);
     for (uint32_t i = lane; i < H; i += 64) cz_rms_store(A, row + i, xs[i] * inv);
 }
 

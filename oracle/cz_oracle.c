@@ -34,6 +34,10 @@
  *                           abs (moe.zig:720-728); determinism.
  *   czo_cache_replay        hand-worked LRU traces (moe.zig:730-741).
  *   czo_chunk_bounds        disjoint cover of [0,n) (parallel.zig:348-375).
+ *   czo_rms_unit /          float64 closed form x / sqrt(mean(x^2) + eps) at
+ *   czo_chain_layer         1e-6; the reference's own rms tests
+ *                           (rmsnorm.zig:67-100 restated as checks); the chain
+ *                           step == rms, then moe.forward, then the residual add.
  */
 #define _GNU_SOURCE
 #include "cz_oracle.h"
@@ -839,24 +843,28 @@ uint32_t czo_cache_replay(uint32_t cap, const uint32_t *ids, size_t n, int32_t *
 }
 
 /* ======================================================================= */
-/* the benchmark's synthetic layer chain                                    */
+/* the decode chain: x <- x + moe(rms(x)) per layer                        */
 /* ======================================================================= */
+/* rmsnorm.zig:32-40 `rms` with a unit weight, the norm qwen3moe/model.zig:228
+ * applies before each MoE block: ss = sum of f64(v)*v over the row (each
+ * square exact in f64), in row order; mean = f32(ss / n); r = 1 / sqrt(mean +
+ * eps) in f32; out_i = x_i * r * w_i with w_i = 1 (an exact multiply). */
+void czo_rms_unit(float *out, const float *x, size_t n, float eps) {
+    double ss = 0.0;
+    for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    const float mean = (float)(ss / (double)n);
+    const float r = 1.0f / sqrtf(mean + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * r * 1.0f;
+}
+
 int czo_chain_layer(const czo_layer *L, float *x, size_t S, float eps, float *xn_out, uint32_t *r_idx,
                     float *r_gate) {
     const uint32_t H = L->d.hidden;
     float *xn = (float *)calloc(S * H, sizeof(float));
     float *o = (float *)calloc(S * H, sizeof(float));
     if (!xn || !o) { free(xn); free(o); return -1; }
-    for (size_t s = 0; s < S; ++s) {
-        const float *xs = x + s * H;
-        float ss = 0;
-        for (uint32_t i = 0; i < H; ++i) {
-            const float sq = xs[i] * xs[i];
-            ss = ss + sq;
-        }
-        const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-        for (uint32_t i = 0; i < H; ++i) xn[s * H + i] = xs[i] * inv;
-    }
+    for (size_t s = 0; s < S; ++s) czo_rms_unit(xn + s * H, x + s * H, H, eps);
+    /* qwen3moe/model.zig:230-232: the MoE block's output added to the residual */
     int rc = czo_moe_forward(L, xn, S, o, r_idx, r_gate);
     if (rc == 0) {
         for (size_t i = 0; i < S * H; ++i) x[i] = x[i] + o[i];

@@ -124,10 +124,12 @@ typedef struct czo_cache_stats {
 uint32_t czo_cache_replay(uint32_t cap, const uint32_t *ids, size_t n, int32_t *slot_out,
                           czo_cache_stats *st);
 
-/* ---- synthetic layer chain used by the benchmark ------------------------ */
-/* x <- x + moe(rms(x)) for one layer, with a unit-weight RMSNorm
- * rms(x)_i = x_i * (1 / sqrtf(sum_f32(x_i^2)/H + eps)).  xn (nullable) gets
- * the router input.  The chain is a workload definition, not reference code. */
+/* ---- the decode chain (qwen3moe/model.zig:228-232 around the MoE block) -- */
+/* rmsnorm.zig:32-40 `rms` with a unit weight: f64 sum of squares, mean
+ * rounded to f32, r = 1/sqrt(mean + eps) in f32, out = x * r. */
+void czo_rms_unit(float *out, const float *x, size_t n, float eps);
+/* x <- x + moe(rms(x)) for one layer (S rows).  xn (nullable) gets the
+ * router input. */
 int czo_chain_layer(const czo_layer *L, float *x, size_t S, float eps, float *xn_out,
                     uint32_t *r_idx, float *r_gate);
 

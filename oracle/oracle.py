@@ -68,6 +68,7 @@ _SIGS = {
     "czo_chunk_bounds": (ctypes.c_uint32, [ctypes.c_size_t, ctypes.c_size_t, vp, ctypes.c_uint32]),
     "czo_cache_replay": (ctypes.c_uint32, [ctypes.c_uint32, vp, ctypes.c_size_t, vp, ctypes.POINTER(CCacheStats)]),
     "czo_chain_layer": (ctypes.c_int, [ctypes.POINTER(CLayer), vp, ctypes.c_size_t, ctypes.c_float, vp, vp, vp]),
+    "czo_rms_unit": (None, [vp, vp, ctypes.c_size_t, ctypes.c_float]),
     "czo_exp_audit": (None, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, vp]),
     "czo_f32fn_compare": (ctypes.c_uint64, [vp, vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, vp]),
 }
@@ -195,6 +196,17 @@ def matmul_bf16(x, w_bits, S, I, O):
     widened exactly (bits << 16), so it is matmul_f32 on the widened matrix."""
     w = (np.ascontiguousarray(w_bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
     return matmul_f32(x, w, S, I, O)
+
+
+def rms_unit(x, eps: float) -> np.ndarray:
+    """rmsnorm.zig:32-40 `rms` with a unit weight, row by row."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    rows = x.reshape(-1, x.shape[-1])
+    o = out.reshape(-1, x.shape[-1])
+    for r in range(rows.shape[0]):
+        lib().czo_rms_unit(_p(o[r]), _p(rows[r]), rows.shape[1], eps)
+    return out
 
 
 def dequant_matrix(w, s):

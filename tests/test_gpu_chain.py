@@ -1,0 +1,166 @@
+"""The decode chain x <- x + MoE(rms(x)) (qwen3moe/model.zig:228-232 with a
+unit-weight rms, rmsnorm.zig:32-40) on the GPU against the oracle's own chain
+run from the same x0: per layer the router input, the routing and the
+residual stream.
+
+Routing bits: both sides evaluate the same correctly rounded f32 exp; the bits
+of the reference's @exp (Zig compiler-rt) and its @reduce lane order cannot be
+observed here.  The near-tie census below records, for every routing decision
+of the oracle, the gap in f32 ulps between consecutive values among the top
+K+1; a gap of at least CENSUS_MIN_ULPS means an exp or a logit off by a few
+ulps on either side cannot reorder the picks, so the indices do not depend on
+those unobserved bits.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from colizig_amd import _lib, moe, synth
+from tests.helpers import f32_bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+RTOL_L2 = 1e-3       # MoE outputs / residual stream vs the CPU path
+CENSUS_MIN_ULPS = 8  # required gap between consecutive top-(K+1) values
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def census_min_gap(v: np.ndarray, K: int) -> int:
+    """Smallest gap, in f32 ulps, between consecutive values of the top K+1
+    (value descending, lowest id first among equals) of the post-exp values v
+    (all >= 0, so their bit patterns order like the values)."""
+    E = v.size
+    order = sorted(range(E), key=lambda e: (-float(v[e]), e))[:min(K + 1, E)]
+    b = f32_bits(v[order]).astype(np.int64)
+    return int(np.min(b[:-1] - b[1:]))
+
+
+def chain_vs_oracle(oracle_lib, hosts, base, S, tokens, eps=1e-6, seed=0, label=""):
+    """Runs the GPU chain and the oracle chain side by side from the same x0;
+    returns (min census gap, max xn rel diff, max residual rel L2)."""
+    nl = len(hosts)
+    H, K = hosts[0]["dims"]["hidden"], hosts[0]["dims"]["topk"]
+    layers = [moe.register_layer(base + l, h) if "registered" not in h else h["registered"]
+              for l, h in enumerate(hosts)]
+    orcs = [oracle_lib.OracleLayer(h) for h in hosts]
+    hip = _lib.hip()
+    x0 = synth.hidden_states(S, H, seed=seed)
+    xb = moe.DeviceBuffer(x0.nbytes)
+    xn_t = moe.DeviceBuffer(nl * x0.nbytes)
+    idx_t = moe.DeviceBuffer(nl * S * K * 4)
+    g_t = moe.DeviceBuffer(nl * S * K * 4)
+    xb.upload(x0)
+    xo = x0.copy()
+    min_gap, worst_xn, worst_x = 1 << 30, 0.0, 0.0
+    for tok in range(tokens):
+        say(f"  {label} token {tok}")
+        rc = hip.colizig_hip_chain_decode(base, nl, xb.ptr, S, eps, xn_t.ptr, idx_t.ptr, g_t.ptr, None)
+        assert rc == 0, _lib.last_error()
+        assert hip.colizig_hip_sync() == 0
+        xn_g = xn_t.download(np.empty((nl, S, H), np.float32))
+        idx_g = idx_t.download(np.empty((nl, S, K), np.uint32))
+        gates_g = g_t.download(np.empty((nl, S, K), np.float32))
+        for l in range(nl):
+            xn_o, idx_o, gates_o = orcs[l].chain(xo, eps)
+            if tok == 0 and l == 0:  # the same x0 on both sides: the same router input, bit for bit
+                assert np.array_equal(f32_bits(xn_g[0]), f32_bits(xn_o)), f"{label}: rms of x0"
+            worst_xn = max(worst_xn, rel_l2(xn_g[l], xn_o))
+            assert rel_l2(xn_g[l], xn_o) < RTOL_L2, f"{label} token {tok} layer {l}: router input"
+            for s in range(S):
+                # the GPU's routing of its own router input == the oracle's, bit for bit
+                ri, rg, _ = orcs[l].route(xn_g[l, s])
+                assert np.array_equal(idx_g[l, s], ri), f"{label} token {tok} layer {l} row {s}: routing"
+                assert np.array_equal(f32_bits(gates_g[l, s]), f32_bits(rg)), f"{label} t{tok} l{l}: gates"
+                # and the same experts as the oracle's own chain picks
+                assert np.array_equal(idx_g[l, s], idx_o[s]), f"{label} token {tok} layer {l} row {s}: picks"
+                _, _, v = orcs[l].route(xn_o[s])
+                min_gap = min(min_gap, census_min_gap(v, K))
+        x_g = xb.download(np.empty_like(x0))
+        worst_x = max(worst_x, rel_l2(x_g, xo))
+        assert rel_l2(x_g, xo) < RTOL_L2, f"{label} token {tok}: residual stream"
+    assert min_gap >= CENSUS_MIN_ULPS, f"{label}: a routing decision within {min_gap} ulps of a tie"
+    say(f"  {label}: census min gap {min_gap} ulps, xn rel diff <= {worst_xn:.2e}, x rel L2 <= {worst_x:.2e}")
+    for b in (xb, xn_t, idx_t, g_t):
+        b.free()
+    return min_gap, worst_xn, worst_x
+
+
+@pytest.mark.parametrize("S", [1, 2, 20])
+def test_chain_vs_oracle_chain_tiny(gpu, oracle_lib, S):
+    """Config-1 shapes (hidden 512, 16 experts, top-4, inter 256), 3 chained
+    layers, 3 steps; S = 1, 2 (decode kernels) and 20 (grouped regime)."""
+    say(f"chain vs oracle chain, tiny S={S}")
+    hosts = [synth.make_layer(512, 16, 4, 256, 0, True, seed=61 + l) for l in range(3)]
+    chain_vs_oracle(oracle_lib, hosts, 1100 + 10 * S, S, tokens=3, seed=S, label=f"tiny S={S}")
+
+
+def test_chain_vs_oracle_chain_qwen3_30b(gpu, oracle_lib):
+    """Qwen3-30B-A3B shapes (hidden 2048, 128 experts, top-8, inter 768) on
+    GPU-generated weights read back for the oracle: 3 chained layers, 4 steps
+    at batch 1, the headline workload's own chain."""
+    say("chain vs oracle chain, qwen3-30b shapes")
+    H, E, K, I = 2048, 128, 8, 768
+    d = moe.dims(H, E, K, I)
+    hosts = []
+    for l in range(3):
+        L = moe.Layer.load(1200 + l, d, np.zeros((E, H), np.float32))
+        L.synth(seed=4321 + l)
+        hosts.append(dict(dims=dict(hidden=H, experts=E, topk=K, inter=I, shared_inter=0, norm_topk=1),
+                          router=L.read_router(), experts=[L.read_expert(e) for e in range(E)], shared=None,
+                          registered=L))
+    chain_vs_oracle(oracle_lib, hosts, 1200, 1, tokens=4, seed=3, label="qwen3-30b")
+
+
+def test_graph_refuses_changed_layers(gpu):
+    """A captured chain graph holds the layers' device pointers: after a layer
+    is re-registered, or its router bias is removed, the graph is refused
+    (-1) and never launched."""
+    say("graph refuses changed layers")
+    hip = _lib.hip()
+    hosts = [synth.make_layer(512, 16, 4, 256, 0, True, seed=71 + l) for l in range(2)]
+    for l, h in enumerate(hosts):
+        moe.register_layer(1300 + l, h)
+    Lb = moe.Layer(1301, moe.Dims(**hosts[1]["dims"]), True)
+    Lb.set_router_bias(np.zeros(16, np.float32))
+    x0 = synth.hidden_states(1, 512, seed=7)
+    xb = moe.DeviceBuffer(x0.nbytes)
+    xb.upload(x0)
+    gh = hip.colizig_hip_chain_graph_create(1300, 2, xb.ptr, 1, 1e-6)
+    assert gh > 0, _lib.last_error()
+    assert hip.colizig_hip_graph_launch(gh, None) == 0
+    assert hip.colizig_hip_sync() == 0
+    Lb.set_router_bias(None)  # frees the bias buffer the graph captured
+    assert hip.colizig_hip_graph_launch(gh, None) == -1
+    assert "changed since capture" in _lib.last_error()
+    hip.colizig_hip_graph_destroy(gh)
+    gh = hip.colizig_hip_chain_graph_create(1300, 2, xb.ptr, 1, 1e-6)
+    assert gh > 0 and hip.colizig_hip_graph_launch(gh, None) == 0
+    assert hip.colizig_hip_sync() == 0
+    moe.register_layer(1300, hosts[0])  # re-registration frees the layer's weights
+    assert hip.colizig_hip_graph_launch(gh, None) == -1
+    hip.colizig_hip_graph_destroy(gh)
+    xb.free()
+
+
+def test_matmul_fp8_key_holding_other_matrix(gpu, oracle_lib):
+    """colizig_cuda_matmul_fp8 with a key whose cache slot holds BF16 rows or
+    an FP8 matrix of another shape: the resident slot is not used as is; the
+    result matches the oracle."""
+    say("keyed matmul over a mismatched slot")
+    rng = np.random.default_rng(17)
+    moe.set_vram_budget(1 << 30)
+    key = moe.Fp8Matrix.expert_key(40, 3, 1)
+    moe.matrix_load_bf16(key, rng.integers(0, 1 << 16, size=(64, 256), dtype=np.uint16))
+    for (O, I) in [(128, 256), (300, 512), (64, 256)]:
+        x = rng.normal(size=(2, I)).astype(np.float32)
+        w, s = synth.block_quantize(rng.normal(0, 0.02, size=(O, I)).astype(np.float32))
+        y = moe.matmul_fp8(x, w, s, 2, I, O, key=key)
+        assert rel_l2(y, oracle_lib.matmul_fp8(x, w, s, 2, I, O)) < 1e-5, (O, I)
+    moe.set_vram_budget(0)

@@ -381,6 +381,67 @@ def test_tiny_qwen3_fixture(oracle_lib):
         assert np.max(np.abs(out - od)) < 1e-3
 
 
+# ---------------------------------------------------------- decode chain ----
+def test_rms_unit_closed_form(oracle_lib):
+    """czo_rms_unit (rmsnorm.zig:32-40 with a unit weight) against the float64
+    closed form x / sqrt(mean(x^2) + eps): a sum in place of the mean, eps
+    outside the square root or a dropped square each miss this by far more
+    than 2e-6."""
+    rng = np.random.default_rng(3)
+    for H, scale in [(512, 1.0), (2048, 1.0), (4096, 30.0), (2048, 1e-3), (7, 2.0)]:
+        x = (rng.normal(size=(3, H)) * scale).astype(np.float32)
+        for eps in (1e-6, 1e-5, 0.1):
+            got = oracle_lib.rms_unit(x, eps)
+            x64 = x.astype(np.float64)
+            want = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + eps)
+            assert np.max(np.abs(got - want) / np.abs(want)) < 2e-6, (H, scale, eps)
+    # rmsnorm.zig:67-73 with a unit (not zero-centred) weight: +-1 rows, eps 0
+    got = oracle_lib.rms_unit(np.array([[1, -1, 1, -1]], np.float32), 0.0)
+    assert np.array_equal(np.abs(got), np.ones((1, 4), np.float32))
+    # eps is added to the mean inside the root: a constant row c -> c / sqrt(c^2 + eps)
+    got = oracle_lib.rms_unit(np.full((1, 16), 3.0, np.float32), 0.25)
+    assert abs(float(got[0, 0]) - 3.0 / np.sqrt(9.25)) < 1e-6
+
+
+def test_rms_unit_is_the_reference_arithmetic(oracle_lib):
+    """Bit-exact against the reference's steps done in numpy: f64 sum of
+    f64(v)*v, mean cast to f32, r = 1/sqrt(mean+eps) in f32, v*r."""
+    rng = np.random.default_rng(9)
+    for H in (512, 2048, 4096):
+        x = rng.normal(size=(4, H)).astype(np.float32)
+        eps = np.float32(1e-6)
+        got = oracle_lib.rms_unit(x, float(eps))
+        for r in range(4):
+            ss = 0.0
+            for v in x[r].astype(np.float64):
+                ss += v * v
+            mean = np.float32(ss / H)
+            inv = np.float32(1.0) / np.sqrt(np.float32(mean + eps), dtype=np.float32)
+            assert np.array_equal(f32_bits(got[r]), f32_bits(x[r] * inv))
+
+
+def test_chain_layer_is_rms_moe_residual(oracle_lib):
+    """czo_chain_layer = rms, then moe.forward on it, then the residual add
+    (qwen3moe/model.zig:228-232), bit for bit; and within 1e-5 of the float64
+    pipeline x + moe_f64(x / sqrt(mean(x^2) + eps))."""
+    host = _layer(seed=5)
+    L = oracle_lib.OracleLayer(host)
+    x = np.random.default_rng(11).normal(size=(3, 512)).astype(np.float32)
+    eps = 1e-6
+    for S in (1, 3):
+        xc = x[:S].copy()
+        xn, idx, gates = L.chain(xc, eps)
+        xn2 = oracle_lib.rms_unit(x[:S], eps)
+        assert np.array_equal(f32_bits(xn), f32_bits(xn2))
+        out, ri, rg = L.forward(xn2)
+        assert np.array_equal(idx, ri) and np.array_equal(f32_bits(gates), f32_bits(rg))
+        assert np.array_equal(f32_bits(xc), f32_bits(x[:S] + out))
+        x64 = x[:S].astype(np.float64)
+        xn64 = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + eps)
+        ref, _ = moe_f64(host, xn64)
+        assert rel_l2(xc, x64 + ref) < 1e-5
+
+
 # ------------------------------------------------------- cache / chunks ----
 def _replay(oracle_lib, cap, ids):
     ids = np.array(ids, np.uint32)
