@@ -70,6 +70,10 @@ SIGNATURES = {
     "colizig_hip_chain_kernel_times": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,
                                                       ctypes.c_float, ctypes.c_int, vp]),
     "colizig_hip_expert_slab_read": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
+    "colizig_hip_set_fused_decode": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_fused_decode_active": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]),
+    "colizig_hip_chain_fused_times": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_float,
+                                                     ctypes.c_int, vp]),
     "colizig_hip_layer_synth": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
     "colizig_hip_expert_read": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp]),
     "colizig_hip_router_read": (ctypes.c_int, [ctypes.c_uint32, vp]),

@@ -6,6 +6,7 @@
 // MXCSR (colizig_cuda.cu:22-29): the GPU runtime must not leak FTZ/DAZ into
 // the engine's CPU float math.
 #include "cz_grouped.h"
+#include "cz_fused.h"
 #include "colizig_hip.h"
 
 #include <xmmintrin.h>
@@ -147,6 +148,22 @@ struct StreamPool {
              prefetch_wasted = 0, bytes_h2d = 0;
 };
 
+// ---- one-launch-per-layer batch-1 decode (cz_fused.h): its device state.
+// Grow-only like Work: captured graphs hold these pointers.
+struct FusedState {
+    bool enabled = true;             // colizig_hip_set_fused_decode
+    int cus = 0;                     // compute units of the device
+    float *r = nullptr;              // [2][H] residual stream (layer inputs), ping-pong
+    float *p = nullptr;              // [2][8][H] per-XCD partial outputs, ping-pong
+    float *zero = nullptr;           // [8][H] zeros: the first layer's partials
+    unsigned long long *lgx = nullptr;  // [8][E] tagged logits
+    unsigned long long *hx = nullptr;   // [K*I] tagged gated products
+    uint32_t *run = nullptr;         // chain-run counter
+    uint32_t *err_host = nullptr;    // host-coherent error word
+    uint32_t *err_dev = nullptr;     // its device address
+    size_t cap_h = 0, cap_e = 0, cap_ki = 0;
+};
+
 struct Ctx {
     int inited = 0;
     char name[192] = {0};
@@ -173,6 +190,7 @@ struct Ctx {
     std::unordered_map<int64_t, hipEvent_t> events;
     int64_t next_handle = 1;
     StreamPool pool;
+    FusedState fused;
 };
 
 Ctx g;
@@ -637,6 +655,138 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     return 0;
 }
 
+LayerHost *find_layer(uint32_t layer);
+
+// The one-launch decode serves batch 1 on a device of 8 XCDs x 32 CUs for
+// resident layers without a shared expert with H in {512, 1024, 2048},
+// E <= 128, K*I a multiple of 1024 with K*I/1024 in {1, 2, 4, 6, 8} and I a
+// multiple of K*I/32 (each wave's down columns within one expert).
+bool fused_ok(const LayerHost &L, int S) {
+    const colizig_dims &d = L.d;
+    if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG) return false;
+    if (d.shared_inter != 0 || d.experts > 128 || d.topk > CZ_MAX_K || d.inter % CZ_BLOCK) return false;
+    if (d.hidden != 512 && d.hidden != 1024 && d.hidden != 2048) return false;
+    const uint64_t ki = (uint64_t)d.topk * d.inter;
+    if (ki % 1024) return false;
+    const uint64_t rw = ki / 1024, cw = ki / 32;
+    if (rw != 1 && rw != 2 && rw != 4 && rw != 6 && rw != 8) return false;
+    return d.inter % cw == 0;
+}
+
+int ensure_fused(const colizig_dims &d) {
+    FusedState &F = g.fused;
+    const size_t ki = (size_t)d.topk * d.inter;
+    if (!F.run) {
+        if (hipMalloc(&F.run, 256) != hipSuccess) return -2;
+        if (hipMemset(F.run, 0, 256) != hipSuccess) return -2;
+        if (hipHostMalloc(&F.err_host, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) return -2;
+        __atomic_store_n(F.err_host, 0u, __ATOMIC_RELEASE);
+        if (hipHostGetDevicePointer((void **)&F.err_dev, F.err_host, 0) != hipSuccess) return -2;
+    }
+    if (F.cap_h < d.hidden) {
+        size_t cap_r = 0, cap_p = 0, cap_z = 0;
+        for (float *q : {F.r, F.p, F.zero})
+            if (q) g.retired.push_back(q);
+        F.r = F.p = F.zero = nullptr;
+        if (grow(&F.r, &cap_r, 2ull * d.hidden) || grow(&F.p, &cap_p, 2ull * CZ_NXCD * d.hidden) ||
+            grow(&F.zero, &cap_z, (size_t)CZ_NXCD * d.hidden))
+            return -2;
+        if (hipMemset(F.zero, 0, cap_z * sizeof(float)) != hipSuccess) return -2;
+        F.cap_h = d.hidden;
+    }
+    if (F.cap_e < d.experts) {
+        size_t cap = 0;
+        if (F.lgx) g.retired.push_back(F.lgx);
+        F.lgx = nullptr;
+        if (grow(&F.lgx, &cap, (size_t)CZ_NXCD * d.experts)) return -2;
+        if (hipMemset(F.lgx, 0, cap * sizeof(unsigned long long)) != hipSuccess) return -2;
+        F.cap_e = d.experts;
+    }
+    if (F.cap_ki < ki) {
+        size_t cap = 0;
+        if (F.hx) g.retired.push_back(F.hx);
+        F.hx = nullptr;
+        if (grow(&F.hx, &cap, ki)) return -2;
+        if (hipMemset(F.hx, 0, cap * sizeof(unsigned long long)) != hipSuccess) return -2;
+        F.cap_ki = ki;
+    }
+    return 0;
+}
+
+template <int NB>
+void launch_fused_nb(const FusedArgs &A, uint32_t rw, hipStream_t st) {
+    switch (rw) {
+        case 1: k_layer_fused<NB, 1><<<CZ_FWG, 256, 0, st>>>(A); return;
+        case 2: k_layer_fused<NB, 2><<<CZ_FWG, 256, 0, st>>>(A); return;
+        case 4: k_layer_fused<NB, 4><<<CZ_FWG, 256, 0, st>>>(A); return;
+        case 6: k_layer_fused<NB, 6><<<CZ_FWG, 256, 0, st>>>(A); return;
+        default: k_layer_fused<NB, 8><<<CZ_FWG, 256, 0, st>>>(A); return;
+    }
+}
+
+// The layers [layer0, layer0 + n) (all fused_ok, one hidden size) as n
+// layer launches and the final residual add.  Residual / partial buffers:
+// layer p reads x_p's parts (x_dev for p <= 1, else r[(p-1) % 2], plus the
+// partials p[(p-1) % 2] for p >= 1), keeps x_p in r[p % 2] (p >= 1) and
+// writes its partials to p[p % 2]; the final kernel writes x_dev.
+int chain_enqueue_fused(uint32_t layer0, uint32_t n, float *x_dev, float eps, float *xn_trace,
+                        uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+    FusedState &F = g.fused;
+    const uint32_t H = find_layer(layer0)->d.hidden;
+    for (uint32_t p = 0; p < n; ++p) {
+        const LayerHost &L = *find_layer(layer0 + p);
+        FusedArgs A{};
+        A.L = L.dev();
+        A.rin = p <= 1 ? x_dev : F.r + (uint64_t)((p - 1) % 2) * H;
+        A.pin = p == 0 ? F.zero : F.p + (uint64_t)((p - 1) % 2) * CZ_NXCD * H;
+        A.has_pin = p == 0 ? 0u : 1u;
+        A.rout = p == 0 ? nullptr : F.r + (uint64_t)(p % 2) * H;
+        A.pout = F.p + (uint64_t)(p % 2) * CZ_NXCD * H;
+        A.lgx = F.lgx;
+        A.hx = F.hx;
+        A.run = F.run;
+        A.err = F.err_dev;
+        A.xn_trace = xn_trace ? xn_trace + (uint64_t)p * H : nullptr;
+        A.idx_trace = idx_trace ? idx_trace + (uint64_t)p * L.d.topk : nullptr;
+        A.gates_trace = gates_trace ? gates_trace + (uint64_t)p * L.d.topk : nullptr;
+        A.pos = p;
+        A.eps = eps;
+        const uint32_t rw = (uint32_t)((uint64_t)L.d.topk * L.d.inter / 1024);
+        switch (H) {
+            case 512: launch_fused_nb<8>(A, rw, st); break;
+            case 1024: launch_fused_nb<16>(A, rw, st); break;
+            default: launch_fused_nb<32>(A, rw, st); break;
+        }
+    }
+    const float *rin_f = n == 1 ? x_dev : F.r + (uint64_t)((n - 1) % 2) * H;
+    k_chain_final<<<(H + 255) / 256, 256, 0, st>>>(x_dev, rin_f, F.p + (uint64_t)((n - 1) % 2) * CZ_NXCD * H, H,
+                                                   F.run);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "fused decode launch: %s", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
+// Whether a chain of n layers from layer0 at S tokens runs the one-launch
+// decode (every layer eligible, one hidden size, < 1023 layers), preparing
+// its buffers; <0 on an allocation failure.
+int chain_fused_prepare(uint32_t layer0, uint32_t n, int S) {
+    if (n >= 1023) return 0;
+    const LayerHost *L0 = find_layer(layer0);
+    if (!L0) return 0;
+    for (uint32_t l = 0; l < n; ++l) {
+        const LayerHost *L = find_layer(layer0 + l);
+        if (!L || !fused_ok(*L, S) || L->d.hidden != L0->d.hidden) return 0;
+    }
+    for (uint32_t l = 0; l < n; ++l) {
+        const int rc = ensure_fused(find_layer(layer0 + l)->d);
+        if (rc) return rc;
+    }
+    return 1;
+}
+
 int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
                  float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
     if (grouped_ok(Lh.d, S))
@@ -677,6 +827,17 @@ int check_layer_ready(LayerHost *L, uint32_t layer) {
     return 0;
 }
 
+// The one-launch decode's error word (set by its kernels when a poll ran
+// out): reported once as -5, then cleared.
+int fused_check_error() {
+    if (!g.fused.err_host) return 0;
+    const uint32_t e = __atomic_exchange_n(g.fused.err_host, 0u, __ATOMIC_ACQ_REL);
+    if (!e) return 0;
+    snprintf(g_err, sizeof g_err, "one-launch decode: an exchange between the workgroups of an XCD timed out "
+             "(error word %#x); the step's results are invalid", e);
+    return -5;
+}
+
 uint64_t mix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ull;
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
@@ -708,6 +869,7 @@ extern "C" int colizig_cuda_init(void) {
     if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return -3;
     snprintf(g.name, sizeof g.name, "%s (%s, %zu MiB)", prop.name, prop.gcnArchName,
              (size_t)(prop.totalGlobalMem >> 20));
+    g.fused.cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) return -4;
     g.budget = 0;  // keyed cache off until set (colizig_cuda.cu:185)
     g.inited = 1;
@@ -755,6 +917,10 @@ extern "C" void colizig_cuda_shutdown(void) {
                     (void *)w.hh, (void *)w.hl, (void *)w.hsh, (void *)w.hsl})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
+    for (void *p : {(void *)g.fused.r, (void *)g.fused.p, (void *)g.fused.zero, (void *)g.fused.lgx,
+                    (void *)g.fused.hx, (void *)g.fused.run})
+        if (p) (void)hipFree(p);
+    if (g.fused.err_host) (void)hipHostFree(g.fused.err_host);
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
     if (P.w) (void)hipFree(P.w);
@@ -1266,6 +1432,9 @@ static int chain_enqueue(uint32_t layer0, uint32_t nlayers, float *x_dev, int S,
         if ((rc = ensure_work(L->d, S))) return rc;
         if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
+    const int fz = chain_fused_prepare(layer0, nlayers, S);
+    if (fz < 0) return fz;
+    if (fz) return chain_enqueue_fused(layer0, nlayers, x_dev, eps, xn_trace, idx_trace, gates_trace, st);
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
         const size_t sh = (size_t)S * L->d.hidden, sk = (size_t)S * L->d.topk;
@@ -1298,6 +1467,7 @@ extern "C" int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlay
         if ((rc = ensure_work(L->d, S))) return rc;
         if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     }
+    if (const int fz = chain_fused_prepare(layer0, nlayers, S); fz < 0) return fz;
     CZ_CHECK(hipStreamSynchronize(g.stream), -4);
     hipGraph_t graph = nullptr;
     CZ_CHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal), -4);
@@ -1560,6 +1730,69 @@ extern "C" int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers,
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (rc && !g_err[0]) snprintf(g_err, sizeof g_err, "kernel timing pass failed (%d)", rc);
+    return rc;
+}
+
+// One-launch decode timing: a HIP graph of `reps` chain steps (n layer
+// launches + the final residual add each) and one of `reps` final kernels
+// alone, each replayed between two events on the library stream; us_out[0] =
+// mean time per layer launch ((chains - finals) / (reps * n)), us_out[1] =
+// mean time of the final kernel.  x_dev advances reps + 1 steps.
+extern "C" int colizig_hip_chain_fused_times(uint32_t layer0, uint32_t nlayers, float *x_dev, float eps, int reps,
+                                             float *us_out) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !x_dev || nlayers == 0 || reps < 1 || !us_out || !dev_aligned(x_dev)) return -1;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        LayerHost *L = find_layer(layer0 + l);
+        int rc = check_layer_ready(L, layer0 + l);
+        if (rc) return rc;
+        if ((rc = ensure_work(L->d, 1))) return rc;
+    }
+    const int fz = chain_fused_prepare(layer0, nlayers, 1);
+    if (fz <= 0) {
+        if (fz == 0) snprintf(g_err, sizeof g_err, "chain is not served by the one-launch decode");
+        return fz < 0 ? fz : -1;
+    }
+    int rc = chain_enqueue_fused(layer0, nlayers, x_dev, eps, nullptr, nullptr, nullptr, g.stream);
+    if (rc) return rc;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    const uint32_t H = find_layer(layer0)->d.hidden;
+    const FusedState &F = g.fused;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    CZ_CHECK(hipEventCreate(&e0), -2);
+    CZ_CHECK(hipEventCreate(&e1), -2);
+    float ms[2] = {0.0f, 0.0f};
+    for (int k = 0; k < 2 && rc == 0; ++k) {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        if (hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { rc = -4; break; }
+        for (int r = 0; r < reps && rc == 0; ++r) {
+            if (k == 0) {
+                rc = chain_enqueue_fused(layer0, nlayers, x_dev, eps, nullptr, nullptr, nullptr, g.stream);
+            } else {
+                k_chain_final<<<(H + 255) / 256, 256, 0, g.stream>>>(x_dev, F.r, F.p, H, F.run);
+                if (hipGetLastError() != hipSuccess) rc = -4;
+            }
+        }
+        const hipError_t ec = hipStreamEndCapture(g.stream, &graph);
+        if (rc == 0 && ec != hipSuccess) rc = -4;
+        if (rc == 0 && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) rc = -4;
+        if (rc == 0 && hipGraphLaunch(exec, g.stream) != hipSuccess) rc = -4;  // warm
+        if (rc == 0 && (hipEventRecord(e0, g.stream) != hipSuccess || hipGraphLaunch(exec, g.stream) != hipSuccess ||
+                        hipEventRecord(e1, g.stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess))
+            rc = -5;
+        if (rc == 0 && hipEventElapsedTime(&ms[k], e0, e1) != hipSuccess) rc = -5;
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc == 0) {
+        us_out[0] = (float)(1000.0 * (ms[0] - ms[1]) / ((double)reps * nlayers));
+        us_out[1] = (float)(1000.0 * ms[1] / reps);
+        rc = fused_check_error();
+    }
     return rc;
 }
 
@@ -2068,11 +2301,30 @@ extern "C" int colizig_hip_memset(void *dst, int value, uint64_t bytes) {
     return 0;
 }
 extern "C" void *colizig_hip_stream(void) { return g.inited ? (void *)g.stream : nullptr; }
+
+extern "C" int colizig_hip_set_fused_decode(int enable) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = g.fused.enabled ? 1 : 0;
+    g.fused.enabled = enable != 0;
+    return prev;
+}
+
+extern "C" int colizig_hip_fused_decode_active(uint32_t layer0, uint32_t nlayers, int S) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || nlayers == 0 || nlayers >= 1023) return 0;
+    const LayerHost *L0 = find_layer(layer0);
+    if (!L0) return 0;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        const LayerHost *L = find_layer(layer0 + l);
+        if (!L || !L->ready() || !fused_ok(*L, S) || L->d.hidden != L0->d.hidden) return 0;
+    }
+    return 1;
+}
 extern "C" int colizig_hip_sync(void) {
     CsrGuard csr;
     if (!g.inited) return -1;
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
-    return 0;
+    return fused_check_error();
 }
 extern "C" int64_t colizig_hip_event_create(void) {
     CsrGuard csr;

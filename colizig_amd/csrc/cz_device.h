@@ -155,6 +155,32 @@ __device__ inline double cz_wave_sum_f64(double v) {
     return v;
 }
 
+template <int CTRL>
+__device__ inline double cz_dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
+    const uint32_t l2 = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xF, 0xF, false);
+    const uint32_t h2 = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)h2 << 32) | l2);
+}
+
+// The same sum through DPP moves inside each 16-lane row, then the four row
+// sums as (r0 + r1) + (r2 + r3); uniform result.
+__device__ inline double cz_wave_sum_f64_dpp(double v) {
+    v = v + cz_dpp_f64<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = v + cz_dpp_f64<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = v + cz_dpp_f64<0x141>(v);  // row_half_mirror
+    v = v + cz_dpp_f64<0x140>(v);  // row_mirror
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
+    double r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r[k] = __builtin_bit_cast(double, ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, 16 * k) << 32) |
+                                              (uint32_t)__builtin_amdgcn_readlane(lo, 16 * k));
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
 // rmsnorm.zig:32-40 `rms` with a unit weight, from ss = the f64 sum of the
 // row's squares (each f64(v)*v is exact in f64, so the sum differs from the
 // reference's row-order sum only by f64 rounding far below an f32 ulp):

@@ -170,7 +170,10 @@ int colizig_hip_chain_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, in
                              uint32_t *idx_trace, float *gates_trace, void *stream);
 
 /* Captures colizig_hip_chain_decode (traces off) into a HIP graph and
- * returns a handle (>0) for colizig_hip_graph_launch; <0 on error. */
+ * returns a handle (>0) for colizig_hip_graph_launch; <0 on error.  The graph
+ * holds the layers' device buffers: colizig_hip_graph_launch returns -1
+ * (launching nothing) once a captured layer has been re-registered, had its
+ * router bias added or removed, or been switched to streaming. */
 int64_t colizig_hip_chain_graph_create(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps);
 int colizig_hip_graph_launch(int64_t handle, void *stream);
 void colizig_hip_graph_destroy(int64_t handle);
@@ -182,6 +185,25 @@ void colizig_hip_graph_destroy(int64_t handle);
  * receives each kernel's mean duration per launch in microseconds. */
 int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps, int reps,
                                    float *us_out);
+
+/* One-launch-per-layer decode.  colizig_hip_chain_decode and its graph run
+ * a batch-1 chain of resident layers as one kernel per layer (plus one final
+ * residual add per chain) when the device has 8 XCDs x 32 CUs and every layer
+ * has no shared expert, hidden 512, 1024 or 2048, at most 128 experts and
+ * K*I a multiple of 1024 with K*I/1024 in {1, 2, 4, 6, 8} and I a multiple
+ * of K*I/32 (the Qwen3-30B-A3B shape and config 1 qualify); otherwise the
+ * three-kernel decode.  Results are the same within the 1e-3 bar, routing
+ * bit-identical.  colizig_hip_set_fused_decode(0) turns it off (returns the
+ * previous setting); colizig_hip_fused_decode_active says whether a chain
+ * would take it.  Its kernels exchange data between workgroups with bounded
+ * waits: a wait that runs out makes the next colizig_hip_sync return -5 (the
+ * step's results are then invalid).  colizig_hip_chain_fused_times: per
+ * layer launch and final-kernel mean durations (us_out[2]) from replayed
+ * graphs of `reps` steps, x_dev advancing.  No counterpart in the reference. */
+int colizig_hip_set_fused_decode(int enable);
+int colizig_hip_fused_decode_active(uint32_t layer0, uint32_t nlayers, int S);
+int colizig_hip_chain_fused_times(uint32_t layer0, uint32_t nlayers, float *x_dev, float eps, int reps,
+                                  float *us_out);
 
 /* ---- streaming tier: experts in pinned host memory, cached in HBM -------
  * ExpertCache (moe.zig:121-249) + loadExpert redesigned for one GPU: one HBM
@@ -268,7 +290,8 @@ int colizig_hip_memcpy_htod(void *dst, const void *src, uint64_t bytes);
 int colizig_hip_memcpy_dtoh(void *dst, const void *src, uint64_t bytes);
 int colizig_hip_memset(void *dst, int value, uint64_t bytes);
 void *colizig_hip_stream(void); /* the library's stream */
-int colizig_hip_sync(void);     /* synchronise the library's stream */
+int colizig_hip_sync(void);     /* synchronise the library's stream; -5 when a one-launch decode step
+                                   since the last call reported an error */
 /* Events on the library stream: create returns a handle; record puts it on
  * `stream` (NULL = library stream); elapsed_ms waits for `b`. */
 int64_t colizig_hip_event_create(void);

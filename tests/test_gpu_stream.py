@@ -1,6 +1,7 @@
 """Streaming tier: experts in pinned host memory, an HBM pool smaller than
-the working set.  A streamed layer runs the same kernels on the same bytes
-as a resident one, so outputs are bit-identical; the pool counters follow
+the working set.  A streamed layer runs the same three-kernel decode on the
+same bytes as a resident one with the one-launch decode switched off, so
+outputs are bit-identical; the pool counters follow
 the cache's invariants (moe.zig:711-741: hits + misses = uses, every miss
 and prefetch is one load)."""
 from __future__ import annotations
@@ -31,9 +32,14 @@ NSLOTS = 16  # = E: one layer's whole selection fits at any S; 4 layers x 16 exp
 
 @pytest.fixture(scope="module")
 def pool(gpu):
-    """One pool per context."""
+    """One pool per context.  The resident side of every comparison runs the
+    streamed tier's three-kernel decode: the one-launch decode is switched
+    off while this module runs and restored after it."""
     moe.stream_pool_init(D, NSLOTS * SLOT)
-    return True
+    hip = _lib.hip()
+    prev = hip.colizig_hip_set_fused_decode(0)
+    yield True
+    hip.colizig_hip_set_fused_decode(prev)
 
 
 def _layers(base_res, base_str, nl, seed, zipf=True):
