@@ -61,6 +61,7 @@ SIGNATURES = {
     "colizig_hip_layer_set_router_bias": (ctypes.c_int, [ctypes.c_uint32, vp]),
     "colizig_hip_moe_forward": (ctypes.c_int, [ctypes.c_uint32, vp, ctypes.c_int, vp, vp, vp]),
     "colizig_hip_moe_forward_dev": (ctypes.c_int, [ctypes.c_uint32, vp, ctypes.c_int, vp, vp, vp, vp]),
+    "colizig_hip_moe_forward_dev_noalloc": (ctypes.c_int, [ctypes.c_uint32, vp, ctypes.c_int, vp, vp, vp, vp]),
     "colizig_hip_chain_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,
                                                 ctypes.c_float, vp, vp, vp, vp]),
     "colizig_hip_chain_graph_create": (ctypes.c_int64, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int,

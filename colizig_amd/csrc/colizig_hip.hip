@@ -838,6 +838,8 @@ int fused_check_error() {
     return -5;
 }
 
+uint8_t *noalloc_scratch();
+
 uint64_t mix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ull;
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
@@ -871,6 +873,9 @@ extern "C" int colizig_cuda_init(void) {
              (size_t)(prop.totalGlobalMem >> 20));
     g.fused.cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) return -4;
+    // the no-alloc forward's scratch address on this device; a failure is
+    // reported by that entry point, which tries again
+    if (!noalloc_scratch()) g_err[0] = 0;
     g.budget = 0;  // keyed cache off until set (colizig_cuda.cu:185)
     g.inited = 1;
     return 0;
@@ -1383,6 +1388,97 @@ extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, i
         return 0;
     }
     return launch_layer(*L, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, idx_dev, gates_dev, pick_stream(stream));
+}
+
+// ---- scratch of colizig_hip_moe_forward_dev_noalloc: one array per GPU,
+// held until the process ends.  In host code `scratch` names a host-side
+// stand-in, never the device memory: kernels and copies take the address
+// hipGetSymbolAddress returns for the current device (noalloc_scratch).
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+uint8_t *g_scratch_dev[kNoAllocMaxDevices] = {};
+
+// Device address of the current device's `scratch`, resolved once per device.
+uint8_t *noalloc_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) {
+        snprintf(g_err, sizeof g_err, "no-alloc forward: no usable current device (%d)", dev);
+        return nullptr;
+    }
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            snprintf(g_err, sizeof g_err, "no-alloc forward: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                     hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_dev[dev] = (uint8_t *)p;
+    }
+    return g_scratch_dev[dev];
+}
+
+// Bytes of scratch a decode-regime forward of S tokens needs; each buffer
+// starts on a 256-byte boundary.
+size_t noalloc_bytes(const colizig_dims &d, int S, size_t off[7]) {
+    const size_t s = (size_t)S;
+    const size_t n[7] = {s * d.hidden * 4,  s * d.experts * 4, s * d.topk * 4, s * d.topk * 4, s * 4,
+                         s * d.topk * (size_t)d.inter * 4, std::max<size_t>(1, s * d.shared_inter) * 4};
+    size_t at = 0;
+    for (int i = 0; i < 7; ++i) {
+        off[i] = at;
+        at += (n[i] + 255) & ~(size_t)255;
+    }
+    return at;
+}
+}  // namespace
+
+extern "C" int colizig_hip_moe_forward_dev_noalloc(uint32_t layer, const float *x_dev, int S, float *out_dev,
+                                                   uint32_t *idx_dev, float *gates_dev, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || S < 1 || !x_dev || !out_dev || !dev_aligned(x_dev, out_dev)) return -1;
+    LayerHost *L = find_layer(layer);
+    int rc = check_layer_ready(L, layer);
+    if (rc) return rc;
+    if (L->streamed()) {
+        snprintf(g_err, sizeof g_err, "no-alloc forward: layer %u is streamed; only resident layers are served",
+                 layer);
+        return -1;
+    }
+    if (grouped_ok(L->d, S)) {
+        snprintf(g_err, sizeof g_err, "no-alloc forward: S=%d takes the grouped regime (S >= %d), which this "
+                 "entry point does not serve", S, kGroupedMinTokens);
+        return -1;
+    }
+    size_t off[7];
+    const size_t need = noalloc_bytes(L->d, S, off);
+    if (need > kNoAllocScratchBytes) {
+        snprintf(g_err, sizeof g_err, "no-alloc forward: S=%d needs %zu bytes of scratch, more than the %zu "
+                 "available", S, need, kNoAllocScratchBytes);
+        return -1;
+    }
+    uint8_t *base = noalloc_scratch();
+    if (!base) return -2;
+    StepArgs A{};
+    A.L = L->dev();
+    A.x = x_dev;
+    A.xn = (float *)(base + off[0]);
+    A.logits = (float *)(base + off[1]);
+    A.idx = (uint32_t *)(base + off[2]);
+    A.gates = (float *)(base + off[3]);
+    A.sgate = (float *)(base + off[4]);
+    A.h = (float *)(base + off[5]);
+    A.hs = (float *)(base + off[6]);
+    A.out = out_dev;
+    A.idx_trace = idx_dev;
+    A.gates_trace = gates_dev;
+    A.S = S;
+    A.tt = router_tokens_per_tile(L->d.hidden);
+    return launch_step(A, pick_stream(stream));
 }
 
 extern "C" int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, uint32_t *routed_idx,

@@ -159,6 +159,20 @@ int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, float *out, u
 int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, int S, float *out_dev, uint32_t *idx_dev,
                                 float *gates_dev, void *stream);
 
+/* No counterpart in the reference.  colizig_hip_moe_forward_dev for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): same arguments, same
+ * kernels, same results, bit for bit.  Its scratch (normalised rows, logits,
+ * routing, expert hidden rows) lives in a static 4 MiB device array per GPU,
+ * held until the process ends; nothing is allocated or freed.  Serves the
+ * decode regime of resident layers: -1 with a message for a streamed layer,
+ * for S that takes the grouped regime, or when
+ * S*(H + E + 2K + 1 + K*I + SI) floats (each part rounded up to 256 bytes)
+ * exceed 4 MiB.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads' streams) race. */
+int colizig_hip_moe_forward_dev_noalloc(uint32_t layer, const float *x_dev, int S, float *out_dev,
+                                        uint32_t *idx_dev, float *gates_dev, void *stream);
+
 /* Decode chain over layers [layer0, layer0+nlayers) on device memory:
  *   x <- x + MoE_l(rmsnorm(x)),  rmsnorm(x)_i = x_i / sqrt(mean(x^2) + eps)
  * (unit-weight RMSNorm; the residual stream the MoE blocks sit in,
