@@ -8,11 +8,14 @@ Workload (one "step" = one decode token through all layers):
   generated on the GPU from a seed; batch 1, hidden state N(0,1).  Layers are
   chained x <- x + MoE_l(rmsnorm(x)) so every layer depends on the previous.
 The timed region replays a HIP graph of one step K times, inputs already in
-HBM.  A second, event-instrumented eager pass gives each kernel's mean
-duration; the gate/up kernel (2/3 of the bytes) is the roofline kernel.
-The CPU baseline runs the oracle (the C restatement of the reference's CPU
-SIMD path, threaded like its parallel.chunks) on the same weights copied to
-host memory, for a bounded number of tokens.
+HBM.  At batch 1 every layer is one kernel launch (router, routing, gate/up,
+SiLU, down and combine); a second graph of the layer launches alone, timed
+with events on the library stream, gives that kernel's mean duration, the
+roofline kernel's.  The parity line runs the oracle's own chain from the same
+x0 over the first layers.  The CPU baseline runs the oracle (the C
+restatement of the reference's CPU SIMD path, threaded like its
+parallel.chunks) on the same weights copied to host memory, for a bounded
+number of tokens.
 
     python bench.py [--steps 256] [--warmup 10] [--cpu-seconds 15] [--no-cpu]
 """
@@ -32,11 +35,11 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
-# HBM bytes per launch of the gate/up kernel on this workload, measured with
-# rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by what the same
-# counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0):
-# 12422.1 KiB fetched, 24.1 KiB written per dispatch.
-UP_TRAFFIC_BYTES = int(round((12399.1 * 2.0 + 48.1) * 1024))
+# HBM bytes per launch of the one-launch layer kernel on this workload,
+# measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by
+# what the same counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0,
+# WRITE_SIZE x 1.0): 23030.8 KiB fetched, 127.8 KiB written per dispatch.
+LAYER_TRAFFIC_BYTES = int(round((23030.8 * 2.0 + 127.8) * 1024))
 
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
@@ -158,24 +161,27 @@ def main():
     tok_s = 1000.0 / ms_per_step
     log(f"timed: {args.steps} steps, {ms_per_step * 1000:.1f} us/token, {tok_s:.1f} tok/s (wall {wall:.3f}s)")
 
-    # per-kernel durations: each kernel kind replayed alone in a HIP graph over
-    # the layers, between two events on the library stream
-    us3 = (ctypes.c_float * 3)()
-    rc = hip.colizig_hip_chain_kernel_times(0, NL, xb.ptr, 1, eps, args.profile_steps, us3)
+    # the layer kernel's duration: a HIP graph of the layer launches replayed
+    # between two events on the library stream (minus the chain's final
+    # residual kernel, timed alone the same way)
+    if hip.colizig_hip_fused_decode_active(0, NL, 1) != 1:
+        raise RuntimeError("the batch-1 chain is not served by the one-launch layer kernel")
+    us2 = (ctypes.c_float * 2)()
+    rc = hip.colizig_hip_chain_fused_times(0, NL, xb.ptr, eps, args.profile_steps, us2)
     if rc != 0:
         raise RuntimeError(f"kernel timing pass failed: {_lib.last_error()}")
-    router_us, up_us, down_us = (float(us3[i]) for i in range(3))
+    layer_us, final_us = float(us2[0]), float(us2[1])
     b = per_token_bytes(c)
-    up_gbs = b["up"] / (up_us * 1e-6) / 1e9
-    down_gbs = b["down"] / (down_us * 1e-6) / 1e9
+    layer_bytes = b["total"]
+    layer_gbs = layer_bytes / (layer_us * 1e-6) / 1e9
     tok_bytes = NL * b["total"]
-    log(f"kernels: router {router_us:.2f} us, gate/up {up_us:.2f} us ({up_gbs:.0f} GB/s), "
-        f"down {down_us:.2f} us ({down_gbs:.0f} GB/s)")
+    log(f"kernels: layer {layer_us:.2f} us ({layer_gbs:.0f} GB/s of {layer_bytes} algorithmic bytes), "
+        f"final residual {final_us:.2f} us")
 
-    # parity spot check on the GPU's own router inputs (first layers)
+    # parity: the oracle's own chain from the same x0 over the first layers
     parity = None
     if args.parity_layers > 0:
-        parity = parity_check(hip, moe, layers[:args.parity_layers], xb, c, eps)
+        parity = parity_check(hip, moe, layers[:args.parity_layers], x0, c, eps)
         log(f"parity: {parity}")
 
     cpu = None
@@ -201,17 +207,16 @@ def main():
         "step_hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_up_fast (top-k + gate/up GEMV + SiLU, 8 experts)",
-            "achieved": round(up_gbs, 1),
+            "kernel": "k_layer_fused (one MoE layer: rmsnorm, router, top-8, gate/up, SiLU, down, combine)",
+            "achieved": round(layer_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(up_gbs / HBM_PEAK_GBS, 4),
-            "traffic": UP_TRAFFIC_BYTES,
-            "bytes_per_launch": b["up"],
-            "avg_launch_us": round(up_us, 3),
+            "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+            "traffic": LAYER_TRAFFIC_BYTES,
+            "bytes_per_launch": layer_bytes,
+            "avg_launch_us": round(layer_us, 3),
         },
-        "kernels_us": {"router": round(router_us, 3), "gate_up": round(up_us, 3), "down": round(down_us, 3),
-                       "down_gbs": round(down_gbs, 1)},
+        "kernels_us": {"layer": round(layer_us, 3), "final_residual": round(final_us, 3)},
         "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
         "parity": parity,
         "cpu_baseline": cpu,
@@ -607,35 +612,40 @@ def calibrate_copy(mib: int) -> None:
     log(f"copied {mib} MiB x 3")
 
 
-def parity_check(hip, moe, layers, xb, c, eps):
-    """Routing of every checked layer bit-exact vs the oracle on the GPU's own
-    router input; MoE output rel L2 vs the oracle."""
+def parity_check(hip, moe, layers, x0, c, eps):
+    """The GPU chain and the oracle's own chain from the same x0 over the
+    given layers, one token: routing bit-exact (on the GPU's router input, and
+    the same picks as the oracle's chain), router input and residual stream
+    within 1e-3 relative L2."""
     from oracle import oracle as orc
-    H, K, E, I = c["hidden"], c["topk"], c["experts"], c["inter"]
+    H, K = c["hidden"], c["topk"]
     n = len(layers)
     xn_t = moe.DeviceBuffer(n * H * 4)
     idx_t = moe.DeviceBuffer(n * K * 4)
-    x = xb.download(np.empty((1, H), np.float32))
+    g_t = moe.DeviceBuffer(n * K * 4)
     xtmp = moe.DeviceBuffer(H * 4)
-    xtmp.upload(x)
-    assert hip.colizig_hip_chain_decode(0, n, xtmp.ptr, 1, eps, xn_t.ptr, idx_t.ptr, None, None) == 0
+    xtmp.upload(x0)
+    assert hip.colizig_hip_chain_decode(0, n, xtmp.ptr, 1, eps, xn_t.ptr, idx_t.ptr, g_t.ptr, None) == 0
     assert hip.colizig_hip_sync() == 0
-    xn = xn_t.download(np.empty((n, 1, H), np.float32))
-    idx = idx_t.download(np.empty((n, 1, K), np.uint32))
-    worst = 0.0
+    xn = xn_t.download(np.empty((n, H), np.float32))
+    idx = idx_t.download(np.empty((n, K), np.uint32))
+    gates = g_t.download(np.empty((n, K), np.float32))
+    x_g = xtmp.download(np.empty((1, H), np.float32))
+    xo = x0.copy()
     exact = True
+    worst_xn = 0.0
     for l, L in enumerate(layers):
-        host = host_layer(hip, L, c)
-        O = orc.OracleLayer(host)
-        ri, _, _ = O.route(xn[l, 0])
-        exact &= bool(np.array_equal(ri, idx[l, 0]))
-        out_g = L.forward(xn[l])[0]
-        out_o = O.forward(xn[l])[0]
-        worst = max(worst, float(np.linalg.norm(out_g - out_o) / np.linalg.norm(out_o)))
-    xn_t.free()
-    idx_t.free()
-    xtmp.free()
-    return {"layers_checked": n, "routing_bit_exact": exact, "max_rel_l2": worst, "tolerance": 1e-3}
+        O = orc.OracleLayer(host_layer(hip, L, c))
+        xn_o, idx_o, _ = O.chain(xo, eps)
+        worst_xn = max(worst_xn, float(np.linalg.norm(xn[l] - xn_o[0]) / np.linalg.norm(xn_o[0])))
+        ri, rg, _ = O.route(xn[l])
+        exact &= bool(np.array_equal(ri, idx[l]) and np.array_equal(rg.view(np.uint32), gates[l].view(np.uint32)))
+        exact &= bool(np.array_equal(idx[l], idx_o[0]))
+    x_err = float(np.linalg.norm(x_g - xo) / np.linalg.norm(xo))
+    for buf in (xn_t, idx_t, g_t, xtmp):
+        buf.free()
+    return {"layers_checked": n, "reference": "oracle chain from the same x0", "routing_bit_exact": exact,
+            "max_router_input_rel_l2": worst_xn, "residual_rel_l2": x_err, "tolerance": 1e-3}
 
 
 def host_layer(hip, L, c):
@@ -666,7 +676,8 @@ def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
     hosts = [orc.OracleLayer(host_layer(hip, L, c)) for L in layers]
     copy_s = time.time() - t0
     # at most 16 host threads per GPU (the CPU share of a one-GPU host), whatever the affinity mask shows
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    present = len(os.sched_getaffinity(0))
+    threads = min(present, 16)
     orc.lib().czo_parallel_enable(threads)
     x = x0.copy()
     n = 0
@@ -679,18 +690,30 @@ def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
             break
     el = time.perf_counter() - t1
     orc.lib().czo_parallel_disable()
-    model = ""
+    return {"value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cores_present": present,
+            "sample": f"{n} decode tokens x {len(layers)} layers of the same workload (oracle chain, "
+                      f"expert fan-out over min(threads, top-k) tasks as parallel.chunks), {el:.1f}s",
+            "cpu_model": cpu_model(), "host_copy_s": round(copy_s, 1)}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode tokens x {len(layers)} layers of the same workload (oracle chain, "
-                      f"expert fan-out over min(threads, top-k) tasks as parallel.chunks), {el:.1f}s",
-            "cpu_model": model, "host_copy_s": round(copy_s, 1)}
+    return ""
 
 
 if __name__ == "__main__":

@@ -83,6 +83,15 @@ __device__ inline float cz_silu_fast(float x) {
 // weight is then ONE f32 multiply by the 128x128 block scale, the definition
 // fp8.zig:105 uses.
 // ---------------------------------------------------------------------------
+// 16 bytes of streamed weights, loaded non-temporal: they are read once per
+// token, so they should not displace what the caches hold for the next steps
+// (router rows, exchanged values, activations).
+__device__ inline uint4 cz_ld_nt16(const uint8_t *p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ inline cz_float2 cz_fp8x2_lo(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false); }
 __device__ inline cz_float2 cz_fp8x2_hi(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true); }
 

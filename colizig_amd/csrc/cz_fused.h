@@ -30,7 +30,8 @@
 // 4 waves x E/4 candidates, identical to moe.zig:447-460's strict '>' scan);
 // then every gate/up row and down row this workgroup needs is requested at
 // once (96 KB + 48 KB at the Qwen3-30B-A3B shape), so the layer's 37.7 MB of
-// expert weights are streamed in one pass; the gated products of the XCD;
+// expert weights are streamed in one pass, and the gates are formed while
+// they arrive; the gated products of the XCD;
 // the down partial of 64 output rows.  Every poll is bounded by the wall
 // clock: a poll that runs out sets a word in host memory (the host reports
 // it) and the kernel finishes with whatever it read, so no wave waits
@@ -87,15 +88,17 @@ __device__ inline void cz_poll_tagged(const unsigned long long *p, uint32_t n, u
     const long long t0 = wall_clock64();
     for (;;) {
         asm volatile("buffer_inv sc0" ::: "memory");  // this CU's L1 holds nothing stale of p
+        // every word requested before the first is waited for (relaxed
+        // atomic loads: one round trip per poll, not one per word)
+        unsigned long long v[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+            v[q] = __hip_atomic_load(p + min(lane + 64u * q, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         bool ok = true;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const uint32_t i = lane + 64u * q;
-            if (i < n) {
-                const unsigned long long v = *(const volatile unsigned long long *)(p + i);
-                out[q] = __builtin_bit_cast(float, (uint32_t)v);
-                ok = ok && (uint32_t)(v >> 32) == tag;
-            }
+            out[q] = __builtin_bit_cast(float, (uint32_t)v[q]);
+            ok = ok && (uint32_t)(v[q] >> 32) == tag;
         }
         if (__builtin_amdgcn_ballot_w64(!ok) == 0) return;  // wave-uniform
         if (wall_clock64() - t0 > CZ_FPOLL_TICKS) {           // a scalar clock: the same in every lane
@@ -106,20 +109,27 @@ __device__ inline void cz_poll_tagged(const unsigned long long *p, uint32_t n, u
     }
 }
 
-// Routing of the token from its E logits (E <= 128), by the whole workgroup:
-// every wave holds all logits (lane l: experts l and l + 64), forms mx, v =
-// exp(l - mx) and the 64-bit keys (bits(v) + 1) << 32 | ~id (0 for NaN or
-// past E), which order the experts exactly as moe.zig:447-460's scan picks
-// them (larger value first, lower id first among equals), so an expert's pick
-// position is the number of keys above its own.  Wave 0 puts the keys in
-// LDS; wave q counts, for each expert, the keys above it among candidates
-// 32 q .. 32 q + 31 (broadcast reads, independent compares); the four counts
-// are summed per expert, and an expert whose count z is < K is pick z.  With
-// fewer than K valid experts the scan's remaining picks are expert 0 (value
-// v[0]).  Gates: top = sum of f64(v) of the picks in pick order, den =
+// Routing of the token from its E logits (E <= 128), by the whole workgroup,
+// in two parts so that the weight loads can be issued between them.
+// cz_route_picks: every wave holds all logits (lane l: experts l and l + 64),
+// forms mx, v = exp(l - mx) and the 64-bit keys (bits(v) + 1) << 32 | ~id (0
+// for NaN or past E), which order the experts exactly as moe.zig:447-460's
+// scan picks them (larger value first, lower id first among equals), so an
+// expert's pick position is the number of keys above its own.  Wave 0 puts
+// the keys in LDS; wave q counts, for each expert, the keys above it among
+// candidates 32 q .. 32 q + 31 (broadcast reads, independent compares); the
+// four counts are summed per expert, and an expert whose count z is < K is
+// pick z.  With fewer than K valid experts the scan's remaining picks are
+// expert 0 (value v[0]).  R.idx[K] is in LDS after its final barrier.
+// cz_route_gates: top = sum of f64(v) of the picks in pick order, den =
 // norm_topk ? top : sum of f64(v_e) in expert order, gate = f32(f64(v) /
-// den).  Results in LDS R.idx[K], R.gate[K] after the final barrier (every
-// thread reaches every barrier).
+// den) into R.gate[K], in LDS after its barrier.  Every thread reaches every
+// barrier of both.
+struct RoutePick {
+    uint32_t nvalid;  // experts with a non-NaN value
+    float v0;         // v of expert 0
+};
+
 struct RouteLds {
     unsigned long long key[128];
     uint32_t cnt[4][128];
@@ -130,7 +140,8 @@ struct RouteLds {
     double all;
 };
 
-__device__ inline void cz_route_wg(const float (&lg)[2], uint32_t E, uint32_t K, uint32_t norm_topk, RouteLds &R) {
+__device__ inline RoutePick cz_route_picks(const float (&lg)[2], uint32_t E, uint32_t K, uint32_t norm_topk,
+                                           RouteLds &R) {
     const uint32_t lane = cz_lane();
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     float v[2];
@@ -177,20 +188,24 @@ __device__ inline void cz_route_wg(const float (&lg)[2], uint32_t E, uint32_t K,
     if (threadIdx.x < 128 && threadIdx.x < E && R.key[threadIdx.x] != 0) {
         const uint32_t e = threadIdx.x;
         const uint32_t z = ((R.cnt[0][e] + R.cnt[1][e]) + R.cnt[2][e]) + R.cnt[3][e];
-        if (z < K) {
+        if (z < K) {  // z < nvalid
             R.idx[z] = e;
             R.val[z] = R.v[e];
         }
     }
+    if (threadIdx.x < K && threadIdx.x >= nvalid) R.idx[threadIdx.x] = 0;  // the scan's pick when nothing is left
     __syncthreads();
+    return RoutePick{nvalid, v0};
+}
+
+__device__ inline void cz_route_gates(const RoutePick &P, uint32_t K, uint32_t norm_topk, RouteLds &R) {
     if (threadIdx.x < K) {
         const uint32_t z = threadIdx.x;
         double top = 0.0;
-        for (uint32_t y = 0; y < K; ++y) top += (double)(y < nvalid ? R.val[y] : v0);
-        const float vz = z < nvalid ? R.val[z] : v0;
+        for (uint32_t y = 0; y < K; ++y) top += (double)(y < P.nvalid ? R.val[y] : P.v0);
+        const float vz = z < P.nvalid ? R.val[z] : P.v0;
         const double den = norm_topk ? top : R.all;
         R.gate[z] = (float)((double)vz / den);
-        if (z >= nvalid) R.idx[z] = 0;  // the scan's pick when nothing is left
     }
     __syncthreads();
 }
@@ -220,8 +235,13 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
 
-    __shared__ __align__(16) float s_x[H];                  // x, then xn
-    __shared__ __align__(16) float s_r[CZ_FEPW * H];        // this workgroup's router rows
+    // xn, and xn and the router rows chain-major for the dotF32 chains: chain
+    // j (elements j + 32 i, i < H/32) is one row of RS floats (RS = H/32 + 4
+    // puts the 16-byte reads of 16 consecutive chains in distinct banks)
+    constexpr uint32_t RS = H / 32 + 4;
+    __shared__ __align__(16) float s_x[H];
+    __shared__ __align__(16) float s_xt[32 * RS];
+    __shared__ __align__(16) float s_rc[CZ_FEPW * 32 * RS];
     __shared__ __align__(16) float s_h[CR];                 // the XCD's gated products
     __shared__ float s_sc[4][2 * (H / CZ_BLOCK) * RW];      // each wave's gate/up block scales
     __shared__ double s_ss[4];
@@ -274,9 +294,16 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     }
     ss = cz_wave_sum_f64_dpp(ss);
     if (lane == 0) s_ss[wave] = ss;
-    // router rows to LDS (rows past ne are never read); they arrive after the residual
+    // router rows to LDS, chain-major (rows past ne are never read); they arrive after the residual
 #pragma unroll
-    for (uint32_t q = 0; q < QR; ++q) reinterpret_cast<cz_f4 *>(s_r)[tid + 256 * q] = rr[q];
+    for (uint32_t q = 0; q < QR; ++q) {
+        const uint32_t f = tid + 256 * q, row = f / H4, c = 4 * (f % H4);  // elements c .. c + 3 of the row
+        float *d = s_rc + (row * 32 + c % 32) * RS + c / 32;
+        d[0] = rr[q].x;
+        d[RS] = rr[q].y;
+        d[2 * RS] = rr[q].z;
+        d[3 * RS] = rr[q].w;
+    }
     __syncthreads();
     const float inv = cz_rms_inv(((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3], H, A.eps);
 #pragma unroll
@@ -286,6 +313,11 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
             const cz_f4 v = xv4[q];
             const cz_f4 y = v * inv;
             reinterpret_cast<cz_f4 *>(s_x)[i] = y;
+            float *d = s_xt + (4 * i % 32) * RS + 4 * i / 32;
+            d[0] = y.x;
+            d[RS] = y.y;
+            d[2 * RS] = y.z;
+            d[3 * RS] = y.w;
             if (blockIdx.x == 0) {
                 if (A.rout) reinterpret_cast<cz_f4 *>(A.rout)[i] = v;
                 if (A.xn_trace) reinterpret_cast<cz_f4 *>(A.xn_trace)[i] = y;
@@ -297,10 +329,17 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     // ---- router logits of experts e0 .. e0 + ne - 1 (dotF32 order, cz_router_combine)
     if (wave < (ne + 1) / 2) {  // half-wave hw of wave q owns expert e0 + 2 q + hw
         const uint32_t hw = lane >> 5, j = lane & 31, el = min(2 * wave + hw, ne - 1);
-        const float *xr = s_x + j, *wr = s_r + el * H + j;
+        const cz_f4 *xr = reinterpret_cast<const cz_f4 *>(s_xt + j * RS);
+        const cz_f4 *wr = reinterpret_cast<const cz_f4 *>(s_rc + (el * 32 + j) * RS);
         float acc = 0.0f;
-#pragma unroll 16
-        for (uint32_t i = 0; i < H / 32; ++i) acc = __builtin_fmaf(xr[32 * i], wr[32 * i], acc);
+#pragma unroll
+        for (uint32_t q = 0; q < H / 128; ++q) {  // elements j + 32 i, i = 4 q .. 4 q + 3, in order
+            const cz_f4 a = xr[q], b = wr[q];
+            acc = __builtin_fmaf(a.x, b.x, acc);
+            acc = __builtin_fmaf(a.y, b.y, acc);
+            acc = __builtin_fmaf(a.z, b.z, acc);
+            acc = __builtin_fmaf(a.w, b.w, acc);
+        }
         float lgt = cz_router_combine(acc, j, hw * 32);
         const uint32_t e = e0 + 2 * wave + hw;
         if (L.router_bias) lgt = lgt + L.router_bias[min(e, E - 1)];
@@ -310,11 +349,7 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     // ---- the XCD's logits, routing
     float lg[2] = {0.0f, 0.0f};
     cz_poll_tagged<2>(A.lgx + (uint64_t)xcd * E, E, tag, lg, A.err);
-    cz_route_wg(lg, E, K, L.norm_topk, s_rt);
-    if (blockIdx.x == 0 && tid < K) {
-        if (A.idx_trace) A.idx_trace[tid] = s_idx[tid];
-        if (A.gates_trace) A.gates_trace[tid] = s_gate[tid];
-    }
+    const RoutePick pick = cz_route_picks(lg, E, K, L.norm_topk, s_rt);
 
     // ---- every weight this workgroup needs, requested at once: the block
     // scales of the wave's rows first (gathered, 64 to a load), then the
@@ -324,14 +359,13 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     constexpr uint32_t NBH = H / CZ_BLOCK;                // scale blocks of a gate/up row
     constexpr uint32_t NSG = 2 * NBH * RW, NSQ = (NSG + 63) / 64;
     uint64_t slr[RW];
-    uint32_t jr[RW];
-    float gz[RW];
+    uint32_t jr[RW], zr[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
         const uint32_t f = f0 + r, z = min(f / I, K - 1);
+        zr[r] = z;
         jr[r] = f - z * I;
         slr[r] = cz_slot(L, min(s_idx[z], E - 1));
-        gz[r] = s_gate[z];
     }
     float scg[NSQ];
 #pragma unroll
@@ -374,8 +408,8 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
         for (uint32_t q = 0; q < GQ; ++q) {
             const uint32_t c = 1024 * q + GB * lane;
             if constexpr (GB == 16) {
-                const uint4 a = *reinterpret_cast<const uint4 *>(wg + c);
-                const uint4 b = *reinterpret_cast<const uint4 *>(wg + (uint64_t)I * H + c);
+                const uint4 a = cz_ld_nt16(wg + c);
+                const uint4 b = cz_ld_nt16(wg + (uint64_t)I * H + c);
                 dg[r][4 * q] = a.x; dg[r][4 * q + 1] = a.y; dg[r][4 * q + 2] = a.z; dg[r][4 * q + 3] = a.w;
                 du[r][4 * q] = b.x; du[r][4 * q + 1] = b.y; du[r][4 * q + 2] = b.z; du[r][4 * q + 3] = b.w;
             } else {
@@ -387,6 +421,16 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // the scales and every gate/up row are requested
+
+    // ---- the gates, while the weights are on their way
+    cz_route_gates(pick, K, L.norm_topk, s_rt);
+    float gz[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) gz[r] = s_gate[zr[r]];
+    if (blockIdx.x == 0 && tid < K) {
+        if (A.idx_trace) A.idx_trace[tid] = s_idx[tid];
+        if (A.gates_trace) A.gates_trace[tid] = s_gate[tid];
+    }
 
     // ---- the scales to the lanes that use them
 #pragma unroll
@@ -441,7 +485,7 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
 #pragma unroll
         for (uint32_t p = 0; p < DP; ++p) {
             const uint32_t row = r0 + DR * p + min(dq, DR - 1);
-            dd[p][i] = *reinterpret_cast<const uint4 *>(wd + (uint64_t)row * I);
+            dd[p][i] = cz_ld_nt16(wd + (uint64_t)row * I);
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // every weight load is in flight
@@ -483,21 +527,31 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     for (uint32_t q = 0; q < NQH; ++q)
         if (lane + 64 * q < HQ) s_h[wave * HQ + lane + 64 * q] = hq[q];
     __syncthreads();
+    // each h slice is read once and used for every pass; four independent
+    // chains (k) per pass
+    float ak[DP][4];
 #pragma unroll
-    for (uint32_t p = 0; p < DP; ++p) {
-        float acc = 0.0f;
+    for (uint32_t p = 0; p < DP; ++p)
 #pragma unroll
-        for (int i = 0; i < RW; ++i) {
-            const float4 *hg = reinterpret_cast<const float4 *>(s_h + 128 * i + 16 * dj);
+        for (int k = 0; k < 4; ++k) ak[p][k] = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 hv = hg[k];
-                acc = __builtin_fmaf(hv.x, wq[p][i][4 * k], acc);
-                acc = __builtin_fmaf(hv.y, wq[p][i][4 * k + 1], acc);
-                acc = __builtin_fmaf(hv.z, wq[p][i][4 * k + 2], acc);
-                acc = __builtin_fmaf(hv.w, wq[p][i][4 * k + 3], acc);
+    for (int i = 0; i < RW; ++i) {
+        const float4 *hg = reinterpret_cast<const float4 *>(s_h + 128 * i + 16 * dj);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 hv = hg[k];
+#pragma unroll
+            for (uint32_t p = 0; p < DP; ++p) {
+                ak[p][k] = __builtin_fmaf(hv.x, wq[p][i][4 * k], ak[p][k]);
+                ak[p][k] = __builtin_fmaf(hv.y, wq[p][i][4 * k + 1], ak[p][k]);
+                ak[p][k] = __builtin_fmaf(hv.z, wq[p][i][4 * k + 2], ak[p][k]);
+                ak[p][k] = __builtin_fmaf(hv.w, wq[p][i][4 * k + 3], ak[p][k]);
             }
         }
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < DP; ++p) {
+        float acc = (ak[p][0] + ak[p][1]) + (ak[p][2] + ak[p][3]);
         // sum over the row's 8 lanes (xor 1, xor 2 within quads, then the two quads)
         acc = acc + cz_dpp<0xB1>(acc);
         acc = acc + cz_dpp<0x4E>(acc);
