@@ -49,6 +49,8 @@ SIGNATURES = {
     "colizig_hip_matrix_load": (ctypes.c_int, [ctypes.c_uint64, vp, vp, ctypes.c_int, ctypes.c_int]),
     "colizig_hip_matmul_fp8_dev": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, vp]),
     "colizig_hip_stream_usage": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]),
+    "colizig_hip_usage_read": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]),
+    "colizig_hip_usage_reset": (ctypes.c_int, []),
     "colizig_hip_stream_warm": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]),
     "colizig_hip_stream_evict_all": (ctypes.c_int, []),
     "colizig_hip_matrix_load_bf16": (ctypes.c_int, [ctypes.c_uint64, vp, ctypes.c_int, ctypes.c_int]),

@@ -52,6 +52,7 @@ struct LayerHost {
     float *ss = nullptr;
     float *shg = nullptr;
     float *rbias = nullptr;  // optional router bias [E]
+    unsigned long long *usage = nullptr;  // [E] routed-selection counters (ExpertUsage row)
     // streamed from host memory: experts live in a pinned host slab (same
     // layout as ew/es) and in slots of the HBM expert pool while cached
     const uint8_t *host_ew = nullptr;
@@ -95,6 +96,7 @@ struct LayerHost {
         L.sh_gate = shg;
         L.router_bias = rbias;
         L.slot_map = slot_map_dev;
+        L.usage = usage;
         return L;
     }
 };
@@ -142,7 +144,6 @@ struct StreamPool {
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
     uint32_t seq = 0;
     uint32_t fills_pending = 0;        // fills enqueued on the copy stream since the compute stream last waited
-    std::unordered_map<uint64_t, uint64_t> usage;  // routed-expert counts by pool key (ExpertUsage)
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
              prefetch_wasted = 0, bytes_h2d = 0;
@@ -302,7 +303,7 @@ void free_layer(LayerHost &L) {
         for (void *p : {(void *)L.ew, (void *)L.es})
             if (p) (void)hipFree(p);
     for (void *p : {(void *)L.router, (void *)L.sw, (void *)L.ss, (void *)L.shg, (void *)L.rbias,
-                    (void *)L.slot_map_dev})
+                    (void *)L.slot_map_dev, (void *)L.usage})
         if (p) (void)hipFree(p);
     if (L.slot_map_stage) (void)hipHostFree(L.slot_map_stage);
     L = LayerHost{};
@@ -551,6 +552,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.gates = w.gates;
     G.sgate = w.sgate;
     G.sgate_ready = rms_rows_write_sgate(A) ? 1u : 0u;
+    G.usage = L.usage;
     G.idx_trace = idx_trace;
     G.gates_trace = gates_trace;
     G.counts = w.counts;
@@ -1270,7 +1272,9 @@ extern "C" int colizig_hip_layer_init(uint32_t layer, const colizig_dims *dims, 
     L.gen = ++g.layer_gen;
     if (hipMalloc(&L.router, (size_t)d.experts * d.hidden * sizeof(float)) != hipSuccess ||
         hipMalloc(&L.ew, L.ew_stride() * d.experts) != hipSuccess ||
-        hipMalloc(&L.es, L.es_stride() * d.experts * sizeof(float)) != hipSuccess) {
+        hipMalloc(&L.es, L.es_stride() * d.experts * sizeof(float)) != hipSuccess ||
+        hipMalloc(&L.usage, (size_t)d.experts * sizeof(unsigned long long)) != hipSuccess ||
+        hipMemset(L.usage, 0, (size_t)d.experts * sizeof(unsigned long long)) != hipSuccess) {
         free_layer(L);
         g.layers.erase(layer);
         snprintf(g_err, sizeof g_err, "layer %u: HBM allocation failed", layer);
@@ -1974,7 +1978,6 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
     StreamPool &P = g.pool;
     P.epoch++;
     for (uint32_t e : sel) {
-        P.usage[pool_key(layer, e)]++;
         auto it = P.where.find(pool_key(layer, e));
         if (it != P.where.end()) {
             const uint32_t i = it->second;
@@ -2073,6 +2076,7 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     G.sgate = w.sgate;
     G.sgate_ready = rms_rows_write_sgate(A) ? 1u : 0u;
     G.tok_order = w.tok_order;
+    G.usage = nullptr;  // the expert kernels below route again and count
     G.xh = nullptr;  // routing only: the grouped regime below splits x itself
     G.xl = nullptr;
     // one token: the routing kernel writes the picks into host memory and then
@@ -2239,19 +2243,45 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
     return 0;
 }
 
-// Routed-expert counts of the streamed layers (expert_usage.zig:21-75): one
-// per step in which the expert was selected for the layer.
-extern "C" int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts) {
+// Routed-selection counts of every registered layer (ExpertUsage.bump,
+// expert_usage.zig:39-45, fed by bumpUsage, moe.zig:428-432): each routing
+// kernel adds one per pick of each token; rows of unregistered layers, or
+// of layers with another expert count, read as zeros.  Waits for the
+// library stream.
+extern "C" int colizig_hip_usage_read(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!g.inited || !counts || experts == 0) return -1;
-    const StreamPool &P = g.pool;
-    for (uint32_t l = 0; l < nlayers; ++l)
-        for (uint32_t e = 0; e < experts; ++e) {
-            const auto it = P.usage.find(pool_key(layer0 + l, e));
-            counts[(uint64_t)l * experts + e] = it == P.usage.end() ? 0 : it->second;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        uint64_t *row = counts + (uint64_t)l * experts;
+        const LayerHost *L = find_layer(layer0 + l);
+        if (!L || !L->usage || L->d.experts != experts) {
+            memset(row, 0, experts * sizeof(uint64_t));
+            continue;
         }
+        CZ_CHECK(hipMemcpy(row, L->usage, experts * sizeof(uint64_t), hipMemcpyDeviceToHost), -5);
+    }
     return 0;
+}
+
+// Zeroes every registered layer's routed-selection counters.
+extern "C" int colizig_hip_usage_reset(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    for (auto &kv : g.layers)
+        if (kv.second.usage)
+            CZ_CHECK(hipMemset(kv.second.usage, 0, kv.second.d.experts * sizeof(unsigned long long)), -4);
+    CZ_CHECK(hipDeviceSynchronize(), -5);
+    return 0;
+}
+
+// The streamed layers' counts: the same counters (kept for callers of the
+// streaming tier's priors).
+extern "C" int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts) {
+    return colizig_hip_usage_read(layer0, nlayers, experts, counts);
 }
 
 // Pre-warms the HBM pool from learned priors (warmCaches, expert_usage.zig:

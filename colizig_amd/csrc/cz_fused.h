@@ -350,6 +350,7 @@ __global__ __launch_bounds__(256) void k_layer_fused(FusedArgs A) {
     float lg[2] = {0.0f, 0.0f};
     cz_poll_tagged<2>(A.lgx + (uint64_t)xcd * E, E, tag, lg, A.err);
     const RoutePick pick = cz_route_picks(lg, E, K, L.norm_topk, s_rt);
+    if (blockIdx.x == 0 && tid < K) cz_bump_usage(L.usage, E, s_idx[tid]);
 
     // ---- every weight this workgroup needs, requested at once: the block
     // scales of the wave's rows first (gathered, 64 to a load), then the

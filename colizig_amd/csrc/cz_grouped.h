@@ -69,6 +69,8 @@ struct GroupArgs {
     uint32_t *host_flag;
     uint32_t host_seq;
     uint32_t sgate_ready;      // 1: the RMS rows kernel already wrote sgate
+    unsigned long long *usage; // [E] routed-selection counters to bump, or null (a routing pass
+                               // whose picks another kernel routes and counts again)
 };
 
 // ---------------------------------------------------------------------------
@@ -103,6 +105,7 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     const uint32_t my_e = lane < L.K ? o_id : 0xffffffffu;
     if (lane < L.K) {  // lane z holds one pick; o_pos is its place in pick order
         const uint64_t o = (uint64_t)t * L.K + o_pos;
+        cz_bump_usage(G.usage, L.E, o_id);
         G.idx[o] = o_id;
         G.gates[o] = o_gate;
         if (G.idx_trace) G.idx_trace[o] = o_id;

@@ -46,7 +46,14 @@ struct LayerDev {
     const float *router_bias;  // [E] added to each logit, or null (workload shaping only)
     const int32_t *slot_map;   // [E] HBM pool slot of each expert (layers streamed from
                                // host memory; ew/es then point at the pool), or null
+    unsigned long long *usage; // [E] routed-selection counters (bumpUsage, moe.zig:428-432), or null
 };
+
+// bumpUsage (moe.zig:428-432): one count per pick of a token (all K of them,
+// a repeated pick counted again), by integer vector atomics (order-free).
+__device__ inline void cz_bump_usage(unsigned long long *usage, uint32_t E, uint32_t e) {
+    if (usage && e < E) atomicAdd(usage + e, 1ull);
+}
 
 // Slot of expert e in ew/es: e itself for a resident layer, the pool slot for
 // a streamed one (the host makes every selected expert resident before the
@@ -743,6 +750,7 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         if (z == 0 && it.tile == 0 && wave == 0) {
             for (uint32_t k = lane; k < L.K; k += 64) {
                 const uint64_t o = (uint64_t)it.tok * L.K + k;
+                cz_bump_usage(L.usage, L.E, s_idx[k]);
                 A.idx[o] = s_idx[k];
                 A.gates[o] = s_gate[k];
                 if (A.idx_trace) A.idx_trace[o] = s_idx[k];

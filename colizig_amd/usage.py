@@ -67,13 +67,20 @@ class ExpertUsage:
         return order[::-1]
 
     @staticmethod
-    def from_pool(layer0: int, layers: int, experts: int) -> "ExpertUsage":
-        """The streaming pool's counts since it was created."""
+    def from_device(layer0: int, layers: int, experts: int) -> "ExpertUsage":
+        """The routed-selection counts the device kept for the layers
+        layer0 .. layer0 + layers - 1 (one per pick of each routed token,
+        bumpUsage, moe.zig:428-432)."""
         u = ExpertUsage(layers, experts)
-        rc = _lib.hip().colizig_hip_stream_usage(layer0, layers, experts, u.counts.ctypes.data_as(ctypes.c_void_p))
+        rc = _lib.hip().colizig_hip_usage_read(layer0, layers, experts, u.counts.ctypes.data_as(ctypes.c_void_p))
         if rc != 0:
-            raise GpuBackendError("colizig_hip_stream_usage", rc)
+            raise GpuBackendError("colizig_hip_usage_read", rc)
         return u
+
+    @staticmethod
+    def from_pool(layer0: int, layers: int, experts: int) -> "ExpertUsage":
+        """The streamed layers' counts (the same device counters)."""
+        return ExpertUsage.from_device(layer0, layers, experts)
 
     def warm_pool(self, layer0: int) -> int:
         """warmCaches (expert_usage.zig:137-160) on the HBM pool; returns the

@@ -249,10 +249,19 @@ int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host
  * plain chain, its graph and the read-back hooks refuse them (-1). */
 int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, float *x_dev, int S, float eps);
 
+/* Routed-selection counters of every registered layer (bumpUsage,
+ * src/qwen38/moe.zig:428-432, into ExpertUsage rows, expert_usage.zig:
+ * 39-45): the routing kernels add one per pick of each token with integer
+ * vector atomics.  colizig_hip_usage_read: counts[l * experts + e] for
+ * layers layer0 .. layer0 + nlayers - 1 (zeros for a layer not registered
+ * or of another expert count); waits for the library stream.
+ * colizig_hip_usage_reset: every layer's counters to zero.  -1 bad args. */
+int colizig_hip_usage_read(uint32_t layer0, uint32_t nlayers, uint32_t experts, uint64_t *counts);
+int colizig_hip_usage_reset(void);
+
 /* Learned priors for the streaming tier (src/runtime/expert_usage.zig:
  * ExpertUsage counts, :21-75; warmCaches, :137-180).
- * colizig_hip_stream_usage: counts[l * experts + e] = steps in which layer
- * layer0 + l routed expert e (since the pool was created).
+ * colizig_hip_stream_usage: the same counters as colizig_hip_usage_read.
  * colizig_hip_stream_warm: fills the pool's free slots with the streamed
  * (layer, expert) pairs of non-zero count, hottest first (one pool across
  * layers: the global top, where the reference warms each layer's cache with

@@ -44,7 +44,9 @@ def census_min_gap(v: np.ndarray, K: int) -> int:
 
 def chain_vs_oracle(oracle_lib, hosts, base, S, tokens, eps=1e-6, seed=0, label=""):
     """Runs the GPU chain and the oracle chain side by side from the same x0;
-    returns (min census gap, max xn rel diff, max residual rel L2)."""
+    returns (min census gap, max xn rel diff, max residual rel L2).  The
+    device's routed-selection counters (bumpUsage, moe.zig:428-432) must
+    equal the counts of the oracle chain's picks."""
     nl = len(hosts)
     H, K = hosts[0]["dims"]["hidden"], hosts[0]["dims"]["topk"]
     layers = [moe.register_layer(base + l, h) if "registered" not in h else h["registered"]
@@ -58,6 +60,9 @@ def chain_vs_oracle(oracle_lib, hosts, base, S, tokens, eps=1e-6, seed=0, label=
     g_t = moe.DeviceBuffer(nl * S * K * 4)
     xb.upload(x0)
     xo = x0.copy()
+    E = hosts[0]["dims"]["experts"]
+    assert hip.colizig_hip_usage_reset() == 0
+    picks = np.zeros((nl, E), np.uint64)
     min_gap, worst_xn, worst_x = 1 << 30, 0.0, 0.0
     for tok in range(tokens):
         say(f"  {label} token {tok}")
@@ -69,6 +74,7 @@ def chain_vs_oracle(oracle_lib, hosts, base, S, tokens, eps=1e-6, seed=0, label=
         gates_g = g_t.download(np.empty((nl, S, K), np.float32))
         for l in range(nl):
             xn_o, idx_o, gates_o = orcs[l].chain(xo, eps)
+            np.add.at(picks[l], idx_o.reshape(-1).astype(np.int64), 1)
             if tok == 0 and l == 0:  # the same x0 on both sides: the same router input, bit for bit
                 assert np.array_equal(f32_bits(xn_g[0]), f32_bits(xn_o)), f"{label}: rms of x0"
             worst_xn = max(worst_xn, rel_l2(xn_g[l], xn_o))
@@ -85,6 +91,10 @@ def chain_vs_oracle(oracle_lib, hosts, base, S, tokens, eps=1e-6, seed=0, label=
         x_g = xb.download(np.empty_like(x0))
         worst_x = max(worst_x, rel_l2(x_g, xo))
         assert rel_l2(x_g, xo) < RTOL_L2, f"{label} token {tok}: residual stream"
+    usage = np.zeros((nl, E), np.uint64)
+    assert hip.colizig_hip_usage_read(base, nl, E, usage.ctypes.data) == 0
+    assert np.array_equal(usage, picks), f"{label}: routed-selection counters"
+    assert int(usage.sum()) == tokens * nl * S * K
     assert min_gap >= CENSUS_MIN_ULPS, f"{label}: a routing decision within {min_gap} ulps of a tie"
     say(f"  {label}: census min gap {min_gap} ulps, xn rel diff <= {worst_xn:.2e}, x rel L2 <= {worst_x:.2e}")
     for b in (xb, xn_t, idx_t, g_t):
