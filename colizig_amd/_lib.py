@@ -85,6 +85,23 @@ SIGNATURES = {
     "colizig_hip_layer_stream_from_host": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
     "colizig_hip_stream_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int, ctypes.c_float]),
     "colizig_hip_stream_stats": (ctypes.c_int, [c_u64p, ctypes.c_int]),
+    "colizig_hip_stream_pool_free": (ctypes.c_int, []),
+    "colizig_hip_layer_stream_from_host_packed": (ctypes.c_int, [ctypes.c_uint32, vp]),
+    "colizig_hip_stream_set_predict": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_stream_log": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_stream_log_read": (ctypes.c_int64, [vp, ctypes.c_uint64]),
+    "colizig_hip_sched_create": (ctypes.c_int64, [ctypes.c_uint32]),
+    "colizig_hip_sched_destroy": (None, [ctypes.c_int64]),
+    "colizig_hip_sched_submit": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]),
+    "colizig_hip_sched_next": (ctypes.c_int, [ctypes.c_int64, c_u32p, c_u32p]),
+    "colizig_hip_sched_cancel": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32]),
+    "colizig_hip_sched_has": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32]),
+    "colizig_hip_sched_stats": (ctypes.c_int, [ctypes.c_int64, c_u64p, ctypes.c_int]),
+    "colizig_hip_predictor_create": (ctypes.c_int64, [ctypes.c_uint32]),
+    "colizig_hip_predictor_destroy": (None, [ctypes.c_int64]),
+    "colizig_hip_predictor_record": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, vp, ctypes.c_uint32]),
+    "colizig_hip_predictor_predict": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, vp, ctypes.c_uint32]),
+    "colizig_hip_predictor_stats": (ctypes.c_int, [ctypes.c_int64, c_u64p, c_u64p]),
     "colizig_hip_host_alloc": (vp, [ctypes.c_uint64]),
     "colizig_hip_host_free": (None, [vp]),
     "colizig_hip_expf_dev": (ctypes.c_int, [vp, vp, ctypes.c_int]),

@@ -7,6 +7,7 @@
 // the engine's CPU float math.
 #include "cz_grouped.h"
 #include "cz_fused.h"
+#include "cz_sched.h"
 #include "colizig_hip.h"
 
 #include <xmmintrin.h>
@@ -16,6 +17,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -53,14 +55,16 @@ struct LayerHost {
     float *shg = nullptr;
     float *rbias = nullptr;  // optional router bias [E]
     unsigned long long *usage = nullptr;  // [E] routed-selection counters (ExpertUsage row)
-    // streamed from host memory: experts live in a pinned host slab (same
-    // layout as ew/es) and in slots of the HBM expert pool while cached
+    // streamed from host memory: experts live in pinned host memory (two
+    // slabs in the ew/es layout, or one packed slab of [weights | scales] per
+    // expert) and in slots of the HBM expert pool while cached
     const uint8_t *host_ew = nullptr;
     const float *host_es = nullptr;
+    const uint8_t *host_packed = nullptr;
+    uint64_t pool_ew_stride = 0, pool_es_stride = 0;  // a pool slot, in bytes / floats
     int32_t *slot_map_dev = nullptr;   // [E] device copy of slot_map
     int32_t *slot_map_stage = nullptr; // [E] pinned staging of the upload
     std::vector<int32_t> slot_map;     // [E] pool slot or -1
-    std::vector<uint32_t> last_used;   // experts of the previous step (prefetch prediction)
     std::vector<uint8_t> loaded;
     uint32_t nloaded = 0;
     bool shared_set = false;
@@ -73,7 +77,7 @@ struct LayerHost {
     uint64_t es_stride() const { return 3ull * nblk(d.inter) * nblk(d.hidden); }
     uint64_t sw_bytes() const { return 3ull * d.shared_inter * d.hidden; }
     uint64_t ss_floats() const { return 3ull * nblk(d.shared_inter) * nblk(d.hidden); }
-    bool streamed() const { return host_ew != nullptr; }
+    bool streamed() const { return host_ew != nullptr || host_packed != nullptr; }
     bool ready() const { return (streamed() || nloaded == d.experts) && (d.shared_inter == 0 || shared_set); }
     LayerDev dev() const {
         LayerDev L{};
@@ -89,8 +93,8 @@ struct LayerHost {
         L.router = router;
         L.ew = ew;
         L.es = es;
-        L.ew_stride = ew_stride();
-        L.es_stride = es_stride();
+        L.ew_stride = streamed() ? pool_ew_stride : ew_stride();
+        L.es_stride = streamed() ? pool_es_stride : es_stride();
         L.sw = sw;
         L.ss = ss;
         L.sh_gate = shg;
@@ -123,12 +127,14 @@ struct Work {
 // gate|up|down weights and scales each), a global LRU over (layer, expert)
 // keys, a side stream for the host->HBM fills.  ExpertCache (moe.zig:121-249)
 // redesigned for one pool shared by every streamed layer.
+constexpr size_t kSchedCapacity = 64;  // queued prefetches at most (io.zig:62-63 bounded queue)
+
 struct StreamPool {
     bool on = false;
     colizig_dims d{};
-    uint64_t w_slot = 0, s_slot = 0;  // bytes / floats per slot (= ew_stride / es_stride)
-    uint8_t *w = nullptr;
-    float *s = nullptr;
+    uint64_t w_slot = 0, s_slot = 0;  // bytes of an expert's weights / floats of its scales
+    uint64_t slot_bytes = 0;          // one slot: [weights | scales], a multiple of 16 bytes
+    uint8_t *base = nullptr;          // nslots slots
     uint32_t nslots = 0;
     std::vector<uint64_t> key;         // 1 + (layer << 32 | expert), 0 = free
     std::vector<uint64_t> used;        // LRU clock of the last use (or fill)
@@ -143,6 +149,19 @@ struct StreamPool {
     size_t h_idx_cap = 0;
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
     uint32_t seq = 0;
+    // next-layer routing prediction (one token): device scratch of its
+    // routing, its picks in host-coherent memory and their sequence number
+    bool predict_next = true;
+    float *pred_logits = nullptr, *pred_gates = nullptr, *pred_sgate = nullptr;
+    uint32_t *pred_idx = nullptr, *pred_tord = nullptr;
+    uint32_t *h_pred = nullptr, *h_pflag = nullptr;
+    uint32_t pseq = 0;
+    std::unordered_map<uint32_t, std::vector<uint32_t>> pred_ids;  // layer -> its predicted experts
+    cz::PredStats next_stats;          // next-layer prediction accuracy
+    cz::LastTokenPredictor last_pred{8};
+    cz::Scheduler sched{kSchedCapacity};
+    bool log_on = false;
+    std::vector<uint32_t> log;         // policy ops, 4 words each (op, layer, expert, result)
     uint32_t fills_pending = 0;        // fills enqueued on the copy stream since the compute stream last waited
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
@@ -930,10 +949,11 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (g.fused.err_host) (void)hipHostFree(g.fused.err_host);
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
-    if (P.w) (void)hipFree(P.w);
-    if (P.s) (void)hipFree(P.s);
-    if (P.h_idx) (void)hipHostFree(P.h_idx);
-    if (P.h_flag) (void)hipHostFree(P.h_flag);
+    for (void *p : {(void *)P.base, (void *)P.pred_logits, (void *)P.pred_gates, (void *)P.pred_sgate,
+                    (void *)P.pred_idx, (void *)P.pred_tord})
+        if (p) (void)hipFree(p);
+    for (void *p : {(void *)P.h_idx, (void *)P.h_flag, (void *)P.h_pred, (void *)P.h_pflag})
+        if (p) (void)hipHostFree(p);
     if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
     if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
     if (P.copy) (void)hipStreamDestroy(P.copy);
@@ -1916,15 +1936,32 @@ namespace {
 
 uint64_t pool_key(uint32_t layer, uint32_t e) { return 1ull + (((uint64_t)layer << 32) | e); }
 
-// A slot for a new entry: a free one, else the least recently used slot not
-// pinned by the layer in flight.  Returns nslots when every slot is pinned.
+// Op log of the pool's policy decisions (4 words per op: op, layer, expert,
+// result), replayed by the oracle's LRU restatement in the tests.
+enum PoolOp : uint32_t { kOpEpoch = 0, kOpGet = 1, kOpPrefetch = 2, kOpWarm = 3, kOpClear = 4 };
+constexpr uint32_t kLogHit = 0x80000000u;       // GET result: slot | kLogHit on a hit
+constexpr uint32_t kLogResident = 0xfffffffeu;  // PREFETCH of a resident expert (no-op)
+constexpr uint32_t kLogNoSlot = 0xffffffffu;    // PREFETCH with every slot pinned (dropped)
+
+void pool_log(uint32_t op, uint32_t layer, uint32_t e, uint32_t result) {
+    StreamPool &P = g.pool;
+    if (!P.log_on) return;
+    P.log.insert(P.log.end(), {op, layer, e, result});
+}
+
+uint8_t *slot_w(uint32_t i) { return g.pool.base + (uint64_t)i * g.pool.slot_bytes; }
+
+// A slot for a new entry: the first free one, else the least recently used
+// slot not pinned by the layer in flight (victimSlot, moe.zig:183-197, over
+// one pool for every streamed layer).  Returns nslots when every slot is
+// pinned.
 uint32_t pool_victim() {
     StreamPool &P = g.pool;
     uint32_t best = P.nslots;
     uint64_t bu = ~0ull;
     for (uint32_t i = 0; i < P.nslots; ++i) {
         if (P.key[i] == 0) return i;
-        if (P.pin_epoch[i] == P.epoch) continue;
+        if (P.epoch != 0 && P.pin_epoch[i] == P.epoch) continue;
         if (P.used[i] < bu) {
             bu = P.used[i];
             best = i;
@@ -1944,7 +1981,9 @@ void pool_drop_layer(uint32_t layer) {
         }
 }
 
-// Copies expert e of streamed layer L into slot i on the copy stream.
+// Copies expert e of streamed layer L into slot i on the copy stream (fill,
+// moe.zig:199-217): one copy from a packed host slab, else weights and
+// scales separately.
 int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetch) {
     StreamPool &P = g.pool;
     if (P.key[i] != 0) {
@@ -1952,10 +1991,15 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
         P.evictions++;
         if (P.prefetched[i]) P.prefetch_wasted++;
     }
-    CZ_CHECK(hipMemcpyAsync(P.w + (uint64_t)i * P.w_slot, L.host_ew + (uint64_t)e * P.w_slot, P.w_slot,
-                            hipMemcpyHostToDevice, P.copy), -3);
-    CZ_CHECK(hipMemcpyAsync(P.s + (uint64_t)i * P.s_slot, L.host_es + (uint64_t)e * P.s_slot,
-                            P.s_slot * sizeof(float), hipMemcpyHostToDevice, P.copy), -3);
+    uint8_t *dst = slot_w(i);
+    if (L.host_packed) {
+        CZ_CHECK(hipMemcpyAsync(dst, L.host_packed + (uint64_t)e * P.slot_bytes, P.slot_bytes, hipMemcpyHostToDevice,
+                                P.copy), -3);
+    } else {
+        CZ_CHECK(hipMemcpyAsync(dst, L.host_ew + (uint64_t)e * P.w_slot, P.w_slot, hipMemcpyHostToDevice, P.copy), -3);
+        CZ_CHECK(hipMemcpyAsync(dst + P.w_slot, L.host_es + (uint64_t)e * P.s_slot, P.s_slot * sizeof(float),
+                                hipMemcpyHostToDevice, P.copy), -3);
+    }
     P.fills_pending++;
     P.bytes_h2d += P.w_slot + P.s_slot * sizeof(float);
     P.loads++;
@@ -1967,17 +2011,20 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
     return 0;
 }
 
-// Makes the experts `sel` of streamed layer `layer` resident (hits touch the
-// LRU, misses are filled on the copy stream).  With `Ld` (at most CZ_SEL_ARGS
-// experts, slots and ids below 2^16) their slots go into Ld's argument table and the compute stream
-// waits for the copy stream only if fills are in flight; otherwise the
-// layer's slot map is uploaded on the copy stream and the compute stream waits
-// for all of it.
+// Makes the experts `sel` of streamed layer `layer` resident (get,
+// moe.zig:221-240: hits touch the LRU, misses are filled on the copy stream)
+// and pins them for the layer in flight.  With `Ld` (at most CZ_SEL_ARGS
+// experts, slots and ids below 2^16) their slots go into Ld's argument table
+// and the compute stream waits for the copy stream only if fills are in
+// flight; otherwise the layer's slot map is uploaded on the copy stream and
+// the compute stream waits for all of it.
 int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &sel, hipStream_t st,
                     LayerDev *Ld = nullptr) {
     StreamPool &P = g.pool;
     P.epoch++;
+    pool_log(kOpEpoch, layer, 0, 0);
     for (uint32_t e : sel) {
+        P.sched.cancel(cz::ExpertKey{layer, e});  // demand-served (io.zig:127-137)
         auto it = P.where.find(pool_key(layer, e));
         if (it != P.where.end()) {
             const uint32_t i = it->second;
@@ -1989,6 +2036,7 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
             P.used[i] = ++P.clock;
             P.pin_epoch[i] = P.epoch;
             L.slot_map[e] = (int32_t)i;
+            pool_log(kOpGet, layer, e, i | kLogHit);
             continue;
         }
         P.misses++;
@@ -2000,8 +2048,8 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
         int rc = pool_fill(L, layer, e, i, false);
         if (rc) return rc;
         P.pin_epoch[i] = P.epoch;
-        P.prefetched[i] = 0;
         L.slot_map[e] = (int32_t)i;
+        pool_log(kOpGet, layer, e, i);
     }
     if (Ld && sel.size() <= CZ_SEL_ARGS && P.nslots <= 0x10000u && L.d.experts <= 0x10000u) {
         Ld->sel_n = (uint32_t)sel.size();
@@ -2022,17 +2070,29 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
     return 0;
 }
 
-// Prefetch (LastTokenPredictor, predict.zig:29-90): the experts layer `layer`
-// used at the previous step, filled now if absent, behind the fills the
-// compute stream waits for; slots pinned by the layer in flight are spared.
-int stream_prefetch(LayerHost &L, uint32_t layer) {
+// Services the scheduler's queue (prefetch, moe.zig:244-248): each key not
+// yet resident is filled into a slot the layer in flight does not pin; a key
+// of a layer that is not streamed is dropped; with every slot pinned the
+// rest of the queue is dropped.
+int pool_service() {
     StreamPool &P = g.pool;
-    for (uint32_t e : L.last_used) {
-        if (P.where.count(pool_key(layer, e))) continue;
+    cz::ExpertKey k;
+    while (P.sched.next(&k)) {
+        LayerHost *L = find_layer(k.layer);
+        if (!L || !L->streamed() || k.id >= L->d.experts) continue;
+        if (P.where.count(pool_key(k.layer, k.id))) {
+            pool_log(kOpPrefetch, k.layer, k.id, kLogResident);
+            continue;
+        }
         const uint32_t i = pool_victim();
-        if (i == P.nslots) return 0;
-        int rc = pool_fill(L, layer, e, i, true);
+        if (i == P.nslots) {
+            pool_log(kOpPrefetch, k.layer, k.id, kLogNoSlot);
+            P.sched.clear();
+            return 0;
+        }
+        const int rc = pool_fill(*L, k.layer, k.id, i, true);
         if (rc) return rc;
+        pool_log(kOpPrefetch, k.layer, k.id, i);
     }
     return 0;
 }
@@ -2040,26 +2100,65 @@ int stream_prefetch(LayerHost &L, uint32_t layer) {
 int ensure_h_idx(int S) {
     StreamPool &P = g.pool;
     const size_t kmax = (size_t)S * CZ_MAX_K;
+    if (!P.h_flag) {
+        if (hipHostMalloc(&P.h_flag, 64, hipHostMallocCoherent) != hipSuccess ||
+            hipHostMalloc(&P.h_pflag, 64, hipHostMallocCoherent) != hipSuccess ||
+            hipHostMalloc(&P.h_pred, CZ_MAX_K * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess)
+            return -2;
+        __atomic_store_n(P.h_flag, 0u, __ATOMIC_RELEASE);
+        __atomic_store_n(P.h_pflag, 0u, __ATOMIC_RELEASE);
+        P.seq = P.pseq = 0;
+    }
     if (P.h_idx_cap >= kmax) return 0;
     if (P.h_idx) (void)hipHostFree(P.h_idx);
     P.h_idx = nullptr;
     P.h_idx_cap = 0;
     if (hipHostMalloc(&P.h_idx, kmax * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess) return -2;
     P.h_idx_cap = kmax;
-    if (!P.h_flag) {
-        if (hipHostMalloc(&P.h_flag, 64, hipHostMallocCoherent) != hipSuccess) return -2;
-        __atomic_store_n(P.h_flag, 0u, __ATOMIC_RELEASE);
-        P.seq = 0;
-    }
     return 0;
 }
 
-// One streamed layer: router and routing on the compute stream, the routing
-// read back; once it is on the host (every earlier kernel has then finished)
-// hits, fills of the misses and the slot map; then the next streamed layer's
-// predicted experts start filling behind them, sparing the slots this layer's
-// kernels will read; then the layer's expert kernels, after its fills.
-// Scratch (ensure_work + ensure_work_grouped) and h_idx must be in place.
+// Waits for a routing kernel's host-memory sequence number; now and then
+// checks that the stream is still working (a failed kernel never sets it).
+int wait_host_seq(const uint32_t *flag, uint32_t seq, hipStream_t st, const char *what) {
+    for (uint32_t n = 1;; ++n) {
+        if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == seq) return 0;
+        if ((n & 4095u) == 0) {
+            const hipError_t q = hipStreamQuery(st);
+            if (q == hipSuccess && __atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq) {
+                snprintf(g_err, sizeof g_err, "%s: the routing kernel ended without its flag", what);
+                return -5;
+            }
+            if (q != hipSuccess && q != hipErrorNotReady) {
+                snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(q));
+                return -5;
+            }
+        }
+    }
+}
+
+template <typename F>
+void for_route_groups(uint32_t E, F &&f) {
+    switch (cz_route_groups(E)) {
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 4: f(std::integral_constant<int, 4>{}); break;
+        case 8: f(std::integral_constant<int, 8>{}); break;
+        default: f(std::integral_constant<int, 16>{}); break;
+    }
+}
+
+// One streamed layer.  On the compute stream: router and routing, and at
+// one token the next streamed layer's routing predicted from this layer's
+// router input (that layer's router on this layer's rms(x): the residual
+// stream changes little from one layer to the next).  Once this layer's
+// picks are on the host (every earlier kernel has then finished): hits,
+// demand fills of the misses (HIGH) and the layer's expert kernels, after
+// its fills; then the next layer's predicted experts (MEDIUM) and the ones
+// it routed for the previous token (LOW, LastTokenPredictor) go through the
+// scheduler and fill on the copy stream while this layer's kernels run,
+// sparing the slots they read.  Scratch (ensure_work + ensure_work_grouped)
+// and the host read-back buffers must be in place.
 int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, float *out, int rms, float eps,
                        const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st) {
     StreamPool &P = g.pool;
@@ -2090,32 +2189,36 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         G.host_flag = (uint32_t *)df;
         G.host_seq = ++P.seq;
     }
-    switch (cz_route_groups(A.L.E)) {
-        case 1: launch_route_tokens<1>(G, st); break;
-        case 2: launch_route_tokens<2>(G, st); break;
-        case 4: launch_route_tokens<4>(G, st); break;
-        case 8: launch_route_tokens<8>(G, st); break;
-        default: launch_route_tokens<16>(G, st); break;
+    for_route_groups(A.L.E, [&](auto m) { launch_route_tokens<decltype(m)::value>(G, st); });
+    const bool predict = direct && P.predict_next && next && next->streamed() && next->ready() &&
+                         next->d.hidden == L.d.hidden && next->d.topk <= CZ_MAX_K;
+    if (predict) {
+        StepArgs Pn = step_args(*next, G.xn, 1, nullptr, 0, eps, nullptr, nullptr, nullptr, nullptr);
+        Pn.logits = P.pred_logits;
+        launch_router(Pn, st);
+        GroupArgs G2{};
+        G2.L = Pn.L;
+        G2.S = 1;
+        G2.xn = G.xn;
+        G2.logits = P.pred_logits;
+        G2.idx = P.pred_idx;
+        G2.gates = P.pred_gates;
+        G2.sgate = P.pred_sgate;
+        G2.sgate_ready = 1;
+        G2.tok_order = P.pred_tord;
+        G2.usage = nullptr;
+        void *di = nullptr, *df = nullptr;
+        CZ_CHECK(hipHostGetDevicePointer(&di, P.h_pred, 0), -4);
+        CZ_CHECK(hipHostGetDevicePointer(&df, P.h_pflag, 0), -4);
+        G2.host_idx = (uint32_t *)di;
+        G2.host_flag = (uint32_t *)df;
+        G2.host_seq = ++P.pseq;
+        for_route_groups(next->d.experts, [&](auto m) { launch_route_tokens<decltype(m)::value>(G2, st); });
     }
     const size_t nk = (size_t)S * L.d.topk;
+    CZ_CHECK(hipGetLastError(), -4);
     if (direct) {
-        CZ_CHECK(hipGetLastError(), -4);
-        // the routing is on the critical path: spin on the flag; now and then
-        // check that the stream is still working (a failed kernel never sets it)
-        for (uint32_t n = 1;; ++n) {
-            if (__atomic_load_n(P.h_flag, __ATOMIC_ACQUIRE) == G.host_seq) break;
-            if ((n & 4095u) == 0) {
-                const hipError_t q = hipStreamQuery(st);
-                if (q == hipSuccess && __atomic_load_n(P.h_flag, __ATOMIC_ACQUIRE) != G.host_seq) {
-                    snprintf(g_err, sizeof g_err, "routing read-back: the routing kernel ended without its flag");
-                    return -5;
-                }
-                if (q != hipSuccess && q != hipErrorNotReady) {
-                    snprintf(g_err, sizeof g_err, "routing read-back: %s", hipGetErrorString(q));
-                    return -5;
-                }
-            }
-        }
+        if (int rc = wait_host_seq(P.h_flag, G.host_seq, st, "routing read-back")) return rc;
     } else {
         CZ_CHECK(hipMemcpyAsync(P.h_idx, w.idx, nk * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
         CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
@@ -2134,18 +2237,39 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         const uint32_t e = std::min(P.h_idx[k], L.d.experts - 1);
         if (std::find(sel.begin(), sel.end(), e) == sel.end()) sel.push_back(e);
     }
+    if (direct) {  // score the predictions of this layer's routing (predict.zig:74-90)
+        const auto it = P.pred_ids.find(layer);
+        if (it != P.pred_ids.end()) {
+            P.next_stats.score(it->second, P.h_idx, nk);
+            P.pred_ids.erase(it);
+        }
+        P.last_pred.record(layer, P.h_idx, nk);
+    }
     const bool grouped = grouped_ok(L.d, S);
     StepArgs A2 = A;  // the decode kernels can take the slots in their arguments
     int rc = stream_resident(L, layer, sel, st, grouped ? nullptr : &A2.L);
     if (rc) return rc;
-    L.last_used = sel;
-    if (next && next->streamed() && (rc = stream_prefetch(*next, next_layer))) return rc;
-    if (grouped) return launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st);
-    return launch_step(A2, st, kUp | kDown);
+    rc = grouped ? launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st)
+                 : launch_step(A2, st, kUp | kDown);
+    if (rc) return rc;
+    if (!next || !next->streamed()) return 0;
+    if (predict) {
+        if ((rc = wait_host_seq(P.h_pflag, P.pseq, st, "predicted routing read-back"))) return rc;
+        std::vector<uint32_t> &pred = P.pred_ids[next_layer];
+        pred.clear();
+        for (uint32_t k = 0; k < next->d.topk; ++k) {
+            const uint32_t e = std::min(P.h_pred[k], next->d.experts - 1);
+            if (std::find(pred.begin(), pred.end(), e) == pred.end()) pred.push_back(e);
+        }
+        for (uint32_t e : pred) P.sched.submit(cz::ExpertKey{next_layer, e}, cz::kMedium);
+    }
+    for (uint32_t e : P.last_pred.predict(next_layer)) P.sched.submit(cz::ExpertKey{next_layer, e}, cz::kLow);
+    return pool_service();
 }
 
 }  // namespace
 
+// The pool's configured shape is fixed until colizig_hip_stream_pool_free.
 extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t cap_bytes) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
@@ -2156,56 +2280,109 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
         return -1;
     }
     const colizig_dims d = *dims;
+    if (d.hidden == 0 || d.inter == 0 || d.experts == 0 || d.experts > CZ_MAX_E || d.topk == 0 ||
+        d.topk > CZ_MAX_K) {
+        snprintf(g_err, sizeof g_err, "unsupported pool dims");
+        return -1;
+    }
     const uint64_t w_slot = 3ull * d.inter * d.hidden, s_slot = 3ull * nblk(d.inter) * nblk(d.hidden);
-    const uint64_t per = w_slot + s_slot * sizeof(float);
-    const uint32_t n = (uint32_t)std::min<uint64_t>(cap_bytes / per, 1u << 24);
+    const uint64_t slot_bytes = (w_slot + s_slot * sizeof(float) + 15) / 16 * 16;
+    const uint32_t n = (uint32_t)std::min<uint64_t>(cap_bytes / slot_bytes, 1u << 24);
     if (n < d.topk) {
         snprintf(g_err, sizeof g_err, "pool of %llu bytes holds %u experts < top-k %u", (unsigned long long)cap_bytes,
                  n, d.topk);
         return -1;
     }
-    if (hipMalloc(&P.w, w_slot * n) != hipSuccess || hipMalloc(&P.s, s_slot * n * sizeof(float)) != hipSuccess) {
-        if (P.w) (void)hipFree(P.w);
-        P.w = nullptr;
+    if (hipMalloc(&P.base, slot_bytes * n) != hipSuccess) {
+        P.base = nullptr;
         snprintf(g_err, sizeof g_err, "expert pool allocation of %u slots failed", n);
         return -2;
     }
-    CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);
-    CZ_CHECK(hipEventCreateWithFlags(&P.ev_idx, hipEventDisableTiming), -4);
-    CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy, hipEventDisableTiming), -4);
+    if (!P.pred_logits &&
+        (hipMalloc(&P.pred_logits, CZ_MAX_E * sizeof(float)) != hipSuccess ||
+         hipMalloc(&P.pred_idx, CZ_MAX_K * sizeof(uint32_t)) != hipSuccess ||
+         hipMalloc(&P.pred_gates, CZ_MAX_K * sizeof(float)) != hipSuccess ||
+         hipMalloc(&P.pred_sgate, 64) != hipSuccess ||
+         hipMalloc(&P.pred_tord, CZ_MAX_K * sizeof(uint32_t)) != hipSuccess))
+        return -2;
+    if (!P.copy) {
+        CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);
+        CZ_CHECK(hipEventCreateWithFlags(&P.ev_idx, hipEventDisableTiming), -4);
+        CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy, hipEventDisableTiming), -4);
+    }
     P.d = d;
     P.w_slot = w_slot;
     P.s_slot = s_slot;
+    P.slot_bytes = slot_bytes;
     P.nslots = n;
     P.key.assign(n, 0);
     P.used.assign(n, 0);
     P.prefetched.assign(n, 0);
     P.pin_epoch.assign(n, 0);
+    P.where.clear();
+    P.clock = 0;
+    P.epoch = 0;
+    P.last_pred.set_topk(d.topk);
     P.on = true;
     return 0;
 }
 
-extern "C" int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host_ew,
-                                                  const float *host_es) {
+// Frees the pool: every streamed layer is unregistered first (its host slabs
+// stay the caller's), the counters start again from zero.
+extern "C" int colizig_hip_stream_pool_free(void) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    LayerHost *L = find_layer(layer);
     StreamPool &P = g.pool;
-    if (!g.inited || !L || !host_ew || !host_es || !P.on) return -1;
+    if (!g.inited || !P.on) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    CZ_CHECK(hipStreamSynchronize(P.copy), -5);
+    for (auto it = g.layers.begin(); it != g.layers.end();) {
+        if (it->second.streamed()) {
+            free_layer(it->second);
+            it = g.layers.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    (void)hipFree(P.base);
+    P.base = nullptr;
+    P.on = false;
+    P.nslots = 0;
+    P.key.clear();
+    P.used.clear();
+    P.prefetched.clear();
+    P.pin_epoch.clear();
+    P.where.clear();
+    P.sched = cz::Scheduler(kSchedCapacity);
+    P.last_pred.reset();
+    P.pred_ids.clear();
+    P.next_stats = cz::PredStats{};
+    P.fills_pending = 0;
+    P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
+        P.bytes_h2d = 0;
+    P.log.clear();
+    return 0;
+}
+
+namespace {
+// Points a registered layer at the pool (its experts now live in host memory).
+int stream_layer_setup(LayerHost *L, uint32_t layer) {
+    StreamPool &P = g.pool;
     const colizig_dims &d = L->d;
     if (d.hidden != P.d.hidden || d.inter != P.d.inter) {
         snprintf(g_err, sizeof g_err, "layer %u shape differs from the expert pool's", layer);
         return -1;
     }
     (void)hipStreamSynchronize(g.stream);
+    (void)hipStreamSynchronize(P.copy);
     if (!L->streamed()) {
         if (L->ew) (void)hipFree(L->ew);
         if (L->es) (void)hipFree(L->es);
     }
-    L->host_ew = host_ew;
-    L->host_es = host_es;
-    L->ew = P.w;
-    L->es = P.s;
+    L->ew = P.base;
+    L->es = reinterpret_cast<float *>(P.base + P.w_slot);
+    L->pool_ew_stride = P.slot_bytes;
+    L->pool_es_stride = P.slot_bytes / sizeof(float);
     L->gen = ++g.layer_gen;
     L->slot_map.assign(d.experts, -1);
     if (!L->slot_map_dev && hipMalloc(&L->slot_map_dev, d.experts * sizeof(int32_t)) != hipSuccess) return -2;
@@ -2213,8 +2390,41 @@ extern "C" int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned
     if (!L->slot_map_stage && hipHostMalloc(&L->slot_map_stage, d.experts * sizeof(int32_t), hipHostMallocDefault) !=
                                   hipSuccess)
         return -2;
-    L->last_used.clear();
     pool_drop_layer(layer);
+    return 0;
+}
+}  // namespace
+
+extern "C" int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host_ew,
+                                                  const float *host_es) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || !host_ew || !host_es || !g.pool.on) return -1;
+    const int rc = stream_layer_setup(L, layer);
+    if (rc) return rc;
+    L->host_ew = host_ew;
+    L->host_es = host_es;
+    L->host_packed = nullptr;
+    return 0;
+}
+
+extern "C" int colizig_hip_layer_stream_from_host_packed(uint32_t layer, const unsigned char *host_slab) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    StreamPool &P = g.pool;
+    if (!g.inited || !L || !host_slab || !P.on) return -1;
+    if (P.slot_bytes != P.w_slot + P.s_slot * sizeof(float)) {
+        snprintf(g_err, sizeof g_err, "packed expert stride %llu is not a multiple of 16 bytes",
+                 (unsigned long long)(P.w_slot + P.s_slot * sizeof(float)));
+        return -1;
+    }
+    const int rc = stream_layer_setup(L, layer);
+    if (rc) return rc;
+    L->host_ew = nullptr;
+    L->host_es = nullptr;
+    L->host_packed = host_slab;
     return 0;
 }
 
@@ -2242,7 +2452,6 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
     }
     return 0;
 }
-
 // Routed-selection counts of every registered layer (ExpertUsage.bump,
 // expert_usage.zig:39-45, fed by bumpUsage, moe.zig:428-432): each routing
 // kernel adds one per pick of each token; rows of unregistered layers, or
@@ -2314,6 +2523,7 @@ extern "C" int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32
         if (next_free == P.nslots) break;
         const int rc = pool_fill(*find_layer(k.l), k.l, k.e, next_free, true);
         if (rc) return rc;
+        pool_log(kOpWarm, k.l, k.e, next_free);
         ++warmed;
     }
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
@@ -2336,6 +2546,10 @@ extern "C" int colizig_hip_stream_evict_all(void) {
     }
     P.where.clear();
     P.fills_pending = 0;
+    P.sched.clear();
+    P.pred_ids.clear();
+    P.last_pred.reset();
+    pool_log(kOpClear, 0, 0, 0);
     for (auto &kv : g.layers)
         if (kv.second.streamed()) std::fill(kv.second.slot_map.begin(), kv.second.slot_map.end(), -1);
     return 0;
@@ -2345,10 +2559,148 @@ extern "C" int colizig_hip_stream_stats(uint64_t *out, int n) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     const StreamPool &P = g.pool;
-    const uint64_t v[10] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
-                            P.prefetch_wasted, P.bytes_h2d, P.nslots, (uint64_t)P.where.size()};
+    const cz::SchedStats &s = P.sched.stats();
+    const cz::PredStats &lt = P.last_pred.stats();
+    const uint64_t v[23] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
+                            P.prefetch_wasted, P.bytes_h2d, P.nslots, (uint64_t)P.where.size(),
+                            P.next_stats.predicted, P.next_stats.correct, lt.predicted, lt.correct,
+                            s.submitted, s.deduped, s.upgraded, s.rejected_full, s.serviced[0], s.serviced[1],
+                            s.serviced[2], s.cancelled, s.queue_peak};
     if (!out || n < 1) return -1;
+    for (int i = 0; i < n && i < 23; ++i) out[i] = v[i];
+    return 0;
+}
+
+// Next-layer routing prediction on or off (returns the previous setting).
+extern "C" int colizig_hip_stream_set_predict(int enable) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = g.pool.predict_next ? 1 : 0;
+    g.pool.predict_next = enable != 0;
+    return prev;
+}
+
+// The pool's op log: enable != 0 clears it and starts recording; 0 stops.
+extern "C" int colizig_hip_stream_log(int enable) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    g.pool.log.clear();
+    g.pool.log_on = enable != 0;
+    return 0;
+}
+
+// Copies up to max_ops recorded ops (4 words each) and returns how many the
+// log holds.
+extern "C" int64_t colizig_hip_stream_log_read(uint32_t *out, uint64_t max_ops) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const std::vector<uint32_t> &lg = g.pool.log;
+    const uint64_t n = lg.size() / 4;
+    if (out) memcpy(out, lg.data(), std::min<uint64_t>(n, max_ops) * 4 * sizeof(uint32_t));
+    return (int64_t)n;
+}
+
+// ---- the scheduler and the last-token predictor on their own (host only;
+// no device or init needed): the interfaces of io.zig and predict.zig.
+namespace {
+std::mutex g_obj_mu;
+std::unordered_map<int64_t, cz::Scheduler> g_scheds;
+std::unordered_map<int64_t, cz::LastTokenPredictor> g_preds;
+int64_t g_next_obj = 1;
+}  // namespace
+
+extern "C" int64_t colizig_hip_sched_create(uint32_t capacity) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const int64_t h = g_next_obj++;
+    g_scheds.emplace(h, cz::Scheduler(capacity));
+    return h;
+}
+
+extern "C" void colizig_hip_sched_destroy(int64_t h) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    g_scheds.erase(h);
+}
+
+extern "C" int colizig_hip_sched_submit(int64_t h, uint32_t layer, uint32_t id, int prio) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_scheds.find(h);
+    if (it == g_scheds.end() || prio < 0 || prio > 2) return -1;
+    return it->second.submit(cz::ExpertKey{layer, id}, (cz::Prio)prio) ? 1 : 0;
+}
+
+extern "C" int colizig_hip_sched_next(int64_t h, uint32_t *layer, uint32_t *id) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_scheds.find(h);
+    if (it == g_scheds.end() || !layer || !id) return -1;
+    cz::ExpertKey k;
+    if (!it->second.next(&k)) return 0;
+    *layer = k.layer;
+    *id = k.id;
+    return 1;
+}
+
+extern "C" int colizig_hip_sched_cancel(int64_t h, uint32_t layer, uint32_t id) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_scheds.find(h);
+    if (it == g_scheds.end()) return -1;
+    return it->second.cancel(cz::ExpertKey{layer, id}) ? 1 : 0;
+}
+
+extern "C" int colizig_hip_sched_has(int64_t h, uint32_t layer, uint32_t id) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_scheds.find(h);
+    if (it == g_scheds.end()) return -1;
+    return it->second.has(cz::ExpertKey{layer, id}) ? 1 : 0;
+}
+
+extern "C" int colizig_hip_sched_stats(int64_t h, uint64_t *out, int n) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_scheds.find(h);
+    if (it == g_scheds.end() || !out) return -1;
+    const cz::SchedStats &s = it->second.stats();
+    const uint64_t v[10] = {s.submitted, s.deduped, s.upgraded, s.rejected_full, s.serviced[0], s.serviced[1],
+                            s.serviced[2], s.cancelled, s.queue_peak, it->second.len()};
     for (int i = 0; i < n && i < 10; ++i) out[i] = v[i];
+    return 0;
+}
+
+extern "C" int64_t colizig_hip_predictor_create(uint32_t topk) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const int64_t h = g_next_obj++;
+    g_preds.emplace(h, cz::LastTokenPredictor(topk));
+    return h;
+}
+
+extern "C" void colizig_hip_predictor_destroy(int64_t h) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    g_preds.erase(h);
+}
+
+extern "C" int colizig_hip_predictor_record(int64_t h, uint32_t layer, const uint32_t *ids, uint32_t n) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_preds.find(h);
+    if (it == g_preds.end() || (n && !ids)) return -1;
+    it->second.record(layer, ids, n);
+    return 0;
+}
+
+extern "C" int colizig_hip_predictor_predict(int64_t h, uint32_t layer, uint32_t *out, uint32_t max) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_preds.find(h);
+    if (it == g_preds.end()) return -1;
+    const std::vector<uint32_t> &p = it->second.predict(layer);
+    const uint32_t n = (uint32_t)std::min<size_t>(p.size(), max);
+    if (n && !out) return -1;
+    std::copy(p.begin(), p.begin() + n, out);
+    return (int)n;
+}
+
+extern "C" int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint64_t *correct) {
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_preds.find(h);
+    if (it == g_preds.end()) return -1;
+    if (predicted) *predicted = it->second.stats().predicted;
+    if (correct) *correct = it->second.stats().correct;
     return 0;
 }
 

@@ -291,7 +291,10 @@ class HostBuffer:
 
 
 STREAM_STAT_NAMES = ("hits", "misses", "loads", "evictions", "prefetch_issued", "prefetch_hits",
-                     "prefetch_wasted", "bytes_h2d", "slots", "resident")
+                     "prefetch_wasted", "bytes_h2d", "slots", "resident", "next_predicted", "next_correct",
+                     "last_predicted", "last_correct", "sched_submitted", "sched_deduped", "sched_upgraded",
+                     "sched_rejected_full", "sched_serviced_high", "sched_serviced_medium", "sched_serviced_low",
+                     "sched_cancelled", "sched_queue_peak")
 
 
 def stream_pool_init(d: Dims, cap_bytes: int) -> None:
@@ -323,3 +326,39 @@ def host_expert_slab(d: Dims, experts: list) -> tuple[HostBuffer, HostBuffer]:
 def stream_layer_from_host(layer: int, wb: HostBuffer, sb: HostBuffer) -> None:
     _check("colizig_hip_layer_stream_from_host",
            _lib.hip().colizig_hip_layer_stream_from_host(layer, wb.ptr, sb.ptr))
+
+
+def packed_expert_bytes(d: Dims) -> int:
+    """Bytes of one expert in a packed host slab: weights, then scales."""
+    return 3 * d.inter * d.hidden + 12 * nblk(d.inter) * nblk(d.hidden)
+
+
+def host_expert_slab_packed(d: Dims, ew: np.ndarray, es: np.ndarray) -> HostBuffer:
+    """One pinned slab of E experts, expert e: its gate | up | down bytes
+    (ew[e], 3*I*H bytes) then their scales (es[e], f32)."""
+    E, P = d.experts, packed_expert_bytes(d)
+    w_slot = 3 * d.inter * d.hidden
+    hb = HostBuffer(E * P)
+    a = hb.view(np.uint8).reshape(E, P)
+    a[:, :w_slot] = np.ascontiguousarray(ew, np.uint8).reshape(E, w_slot)
+    a[:, w_slot:] = np.ascontiguousarray(es, np.float32).reshape(E, -1).view(np.uint8)
+    return hb
+
+
+def stream_layer_from_host_packed(layer: int, hb: HostBuffer) -> None:
+    _check("colizig_hip_layer_stream_from_host_packed",
+           _lib.hip().colizig_hip_layer_stream_from_host_packed(layer, hb.ptr))
+
+
+def stream_pool_free() -> None:
+    _check("colizig_hip_stream_pool_free", _lib.hip().colizig_hip_stream_pool_free())
+
+
+def stream_log_read() -> np.ndarray:
+    """The pool's op log as an [n, 4] uint32 array (op, layer, expert, result)."""
+    hip = _lib.hip()
+    n = int(hip.colizig_hip_stream_log_read(None, 0))
+    out = np.zeros((n, 4), np.uint32)
+    if n:
+        hip.colizig_hip_stream_log_read(out.ctypes.data_as(ctypes.c_void_p), n)
+    return out

@@ -222,15 +222,23 @@ int colizig_hip_chain_fused_times(uint32_t layer0, uint32_t nlayers, float *x_de
 /* ---- streaming tier: experts in pinned host memory, cached in HBM -------
  * ExpertCache (moe.zig:121-249) + loadExpert redesigned for one GPU: one HBM
  * pool of fixed-size expert slots shared by every streamed layer, a global
- * LRU over (layer, expert), fills by hipMemcpyAsync from pinned host memory
- * on a side stream that the compute stream waits for, and a last-step
- * predictor (predict.zig:29-90) that starts filling the next layer's likely
- * experts while the current layer computes. */
+ * LRU over (layer, expert) that spares the slots of the layer in flight,
+ * fills by hipMemcpyAsync from pinned host memory on a side stream that the
+ * compute stream waits for.  Prefetches go through a bounded priority queue
+ * (Scheduler, src/runtime/io.zig:58-140): at one token the next streamed
+ * layer's routing is predicted on the device from the current layer's
+ * router input (MEDIUM), and the experts a layer routed for the previous
+ * token (LastTokenPredictor, predict.zig:29-90) are queued LOW; they fill
+ * while the current layer's expert kernels run. */
 
 /* Creates the pool: floor(cap_bytes / slot) slots for experts of shape
- * (dims->hidden, dims->inter), slot = 3*I*H bytes + 3*nblk(I)*nblk(H) floats.
- * Once per context.  -1 when the pool would hold fewer than top-k experts. */
+ * (dims->hidden, dims->inter); a slot holds [3*I*H weight bytes | 3*nblk(I)*
+ * nblk(H) f32 scales], rounded up to 16 bytes.  -1 when the pool would hold
+ * fewer than top-k experts or one is configured already.
+ * colizig_hip_stream_pool_free: unregisters every streamed layer, frees the
+ * pool and zeroes its counters (a new pool may then be created). */
 int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t cap_bytes);
+int colizig_hip_stream_pool_free(void);
 
 /* Makes a registered layer stream its experts from host memory: host_ew /
  * host_es hold all E experts in the HBM slab layout (expert e at e*3*I*H
@@ -239,6 +247,11 @@ int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t cap_bytes);
  * re-registered or the context shut down.  The layer's own HBM expert slab
  * is released. */
 int colizig_hip_layer_stream_from_host(uint32_t layer, const unsigned char *host_ew, const float *host_es);
+
+/* The same with one pinned slab of E experts, expert e at e * P bytes with P
+ * = 3*I*H + 12*nblk(I)*nblk(H): gate | up | down weights, then their scales
+ * (f32), so that a fill is one copy.  -1 when P is not a multiple of 16. */
+int colizig_hip_layer_stream_from_host_packed(uint32_t layer, const unsigned char *host_slab);
 
 /* colizig_hip_chain_decode over layers some of which stream: per streamed
  * layer the routing is read back to the host, misses are filled, the next
@@ -272,9 +285,55 @@ int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts
 int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32_t experts, const uint64_t *counts);
 int colizig_hip_stream_evict_all(void);
 
-/* Pool counters, out[0..n): hits, misses, loads, evictions, prefetch_issued,
- * prefetch_hits, prefetch_wasted, bytes_h2d, slots, resident entries. */
+/* Pool counters, out[0..n) (n <= 23): hits, misses, loads, evictions,
+ * prefetch_issued, prefetch_hits, prefetch_wasted (CacheStats,
+ * moe.zig:121-139), bytes_h2d, slots, resident entries; next-layer
+ * prediction: ids predicted, ids correct; last-token prediction: predicted,
+ * correct (predict.zig:19-27); scheduler (io.zig:38-52): submitted, deduped,
+ * upgraded, rejected_full, serviced HIGH / MEDIUM / LOW, cancelled,
+ * queue_peak. */
 int colizig_hip_stream_stats(uint64_t *out, int n);
+
+/* Next-layer routing prediction on (default) or off; returns the previous
+ * setting. */
+int colizig_hip_stream_set_predict(int enable);
+
+/* Op log of the pool's policy (test hook).  colizig_hip_stream_log(1) clears
+ * and starts it, (0) stops it.  colizig_hip_stream_log_read copies up to
+ * max_ops ops of 4 words (op, layer, expert, result) and returns the count
+ * held.  op 0 = a layer's gets begin (its pins replace the previous layer's),
+ * 1 = demand get (result: slot, | 0x80000000 on a hit), 2 = prefetch
+ * (result: slot filled, 0xfffffffe already resident, 0xffffffff every slot
+ * pinned: dropped), 3 = warm fill of a free slot (result: slot), 4 = every
+ * slot freed. */
+int colizig_hip_stream_log(int enable);
+int64_t colizig_hip_stream_log_read(uint32_t *out, uint64_t max_ops);
+
+/* The streaming tier's policy objects on their own: host code, no device
+ * and no colizig_cuda_init needed.
+ * Scheduler (io.zig:58-140) of expert keys (layer, id): create with a
+ * capacity; submit (prio 0 HIGH, 1 MEDIUM, 2 LOW) returns 1 accepted (a
+ * queued key is deduplicated and takes the stronger priority), 0 refused
+ * (full); next returns 1 and the strongest-priority key (FIFO within a
+ * priority), 0 when empty; cancel / has return 1 or 0; stats out[0..n)
+ * (n <= 10): submitted, deduped, upgraded, rejected_full, serviced HIGH /
+ * MEDIUM / LOW, cancelled, queue_peak, queued.
+ * LastTokenPredictor (predict.zig:29-90): record(layer, ids) scores the
+ * previous prediction of that layer and keeps the first topk ids; predict
+ * copies them (returns how many); stats: ids predicted, ids correct.
+ * -1 on an unknown handle or bad arguments. */
+int64_t colizig_hip_sched_create(uint32_t capacity);
+void colizig_hip_sched_destroy(int64_t h);
+int colizig_hip_sched_submit(int64_t h, uint32_t layer, uint32_t id, int prio);
+int colizig_hip_sched_next(int64_t h, uint32_t *layer, uint32_t *id);
+int colizig_hip_sched_cancel(int64_t h, uint32_t layer, uint32_t id);
+int colizig_hip_sched_has(int64_t h, uint32_t layer, uint32_t id);
+int colizig_hip_sched_stats(int64_t h, uint64_t *out, int n);
+int64_t colizig_hip_predictor_create(uint32_t topk);
+void colizig_hip_predictor_destroy(int64_t h);
+int colizig_hip_predictor_record(int64_t h, uint32_t layer, const uint32_t *ids, uint32_t n);
+int colizig_hip_predictor_predict(int64_t h, uint32_t layer, uint32_t *out, uint32_t max);
+int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint64_t *correct);
 
 /* Pinned host memory for the host expert slabs. */
 void *colizig_hip_host_alloc(uint64_t bytes);

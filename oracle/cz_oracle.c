@@ -842,6 +842,72 @@ uint32_t czo_cache_replay(uint32_t cap, const uint32_t *ids, size_t n, int32_t *
     return resident;
 }
 
+/* ExpertCache over (layer, expert) keys with pins and prefetch marks: the
+ * library's HBM pool policy, restated from moe.zig:141-248 (see the header). */
+int64_t czo_pool_replay(uint32_t nslots, const uint32_t *ops, size_t n, uint32_t *res_out, czo_pool_stats *st) {
+    if (nslots == 0) return -1;
+    uint64_t *key = (uint64_t *)calloc(nslots, sizeof(uint64_t)); /* 0 = empty, else 1 + (layer << 32 | expert) */
+    uint64_t *used = (uint64_t *)calloc(nslots, sizeof(uint64_t));
+    uint64_t *pin = (uint64_t *)calloc(nslots, sizeof(uint64_t));
+    uint8_t *pref = (uint8_t *)calloc(nslots, 1);
+    if (!key || !used || !pin || !pref) abort();
+    uint64_t clock = 0, epoch = 0;
+    czo_pool_stats s;
+    memset(&s, 0, sizeof s);
+    int64_t rc = 0;
+    for (size_t t = 0; t < n && rc == 0; ++t) {
+        const uint32_t op = ops[4 * t], layer = ops[4 * t + 1], e = ops[4 * t + 2];
+        const uint64_t k = 1ull + (((uint64_t)layer << 32) | e);
+        uint32_t res = 0;
+        int32_t at = -1;
+        for (uint32_t i = 0; i < nslots; ++i)
+            if (key[i] == k) { at = (int32_t)i; break; }
+        if (op == 0) {
+            epoch++;
+        } else if (op == 4) {
+            for (uint32_t i = 0; i < nslots; ++i) { key[i] = 0; pref[i] = 0; }
+        } else if (op == 1 && at >= 0) { /* get: hit */
+            s.hits++;
+            if (pref[at]) { s.prefetch_hits++; pref[at] = 0; }
+            used[at] = ++clock;
+            pin[at] = epoch;
+            res = (uint32_t)at | 0x80000000u;
+        } else if (op == 2 && at >= 0) { /* prefetch of a resident expert */
+            res = 0xfffffffeu;
+        } else {
+            /* a fill: get miss, prefetch or warm */
+            int32_t v = -1;
+            for (uint32_t i = 0; i < nslots; ++i)
+                if (key[i] == 0) { v = (int32_t)i; break; }
+            if (v < 0 && op != 3) {
+                for (uint32_t i = 0; i < nslots; ++i) {
+                    if (pin[i] == epoch && epoch != 0) continue;
+                    if (v < 0 || used[i] < used[v]) v = (int32_t)i;
+                }
+            }
+            if (v < 0) {
+                if (op == 1) { rc = -1; break; }
+                res = 0xffffffffu; /* prefetch dropped / no free slot to warm */
+            } else {
+                if (key[v]) { s.evictions++; if (pref[v]) s.prefetch_wasted++; }
+                key[v] = k;
+                used[v] = ++clock;
+                s.loads++;
+                pref[v] = op != 1;
+                if (op != 1) s.prefetch_issued++;
+                if (op == 1) { s.misses++; pin[v] = epoch; }
+                res = (uint32_t)v;
+            }
+        }
+        if (res_out) res_out[t] = res;
+    }
+    int64_t resident = 0;
+    for (uint32_t i = 0; i < nslots; ++i) resident += key[i] != 0;
+    if (st) *st = s;
+    free(key); free(used); free(pin); free(pref);
+    return rc < 0 ? -1 : resident;
+}
+
 /* ======================================================================= */
 /* the decode chain: x <- x + moe(rms(x)) per layer                        */
 /* ======================================================================= */

@@ -124,6 +124,28 @@ typedef struct czo_cache_stats {
 uint32_t czo_cache_replay(uint32_t cap, const uint32_t *ids, size_t n, int32_t *slot_out,
                           czo_cache_stats *st);
 
+/* The same cache over (layer, expert) keys for every streamed layer, as one
+ * pool of `nslots` slots (the library's HBM expert pool), replaying a log of
+ * ops of 4 words (op, layer, expert, result):
+ *   0 begin a layer's gets: the slots the previous layer pinned are free to
+ *     evict again;
+ *   1 get (moe.zig:221-240): a hit touches the LRU clock and consumes a
+ *     prefetch mark; a miss fills a victim; the slot is pinned;
+ *   2 prefetch (moe.zig:244-248): a no-op when resident, else a fill marked
+ *     prefetched; dropped when every slot is pinned;
+ *   3 warm fill into the first free slot (expert_usage.zig:137-160);
+ *   4 every slot freed.
+ * Victim (moe.zig:183-197): the first empty slot, else the least recently
+ * used slot not pinned by the layer in flight; evicting a prefetched slot
+ * counts as wasted.  Writes each op's result in the log's encoding (get:
+ * slot | 0x80000000 on a hit; prefetch: slot, 0xfffffffe resident,
+ * 0xffffffff dropped; warm: slot; others 0) to res_out; returns the number
+ * of resident entries at the end, or -1 when a get finds every slot pinned. */
+typedef struct czo_pool_stats {
+    uint64_t hits, misses, loads, evictions, prefetch_issued, prefetch_hits, prefetch_wasted;
+} czo_pool_stats;
+int64_t czo_pool_replay(uint32_t nslots, const uint32_t *ops, size_t n, uint32_t *res_out, czo_pool_stats *st);
+
 /* ---- the decode chain (qwen3moe/model.zig:228-232 around the MoE block) -- */
 /* rmsnorm.zig:32-40 `rms` with a unit weight: f64 sum of squares, mean
  * rounded to f32, r = 1/sqrt(mean + eps) in f32, out = x * r. */

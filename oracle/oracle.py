@@ -41,6 +41,13 @@ class CCacheStats(ctypes.Structure):
                                                  "prefetch_wasted")]
 
 
+POOL_STAT_NAMES = ("hits", "misses", "loads", "evictions", "prefetch_issued", "prefetch_hits", "prefetch_wasted")
+
+
+class CPoolStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in POOL_STAT_NAMES]
+
+
 _SIGS = {
     "czo_nblk": (ctypes.c_size_t, [ctypes.c_size_t]),
     "czo_e4m3_decode": (ctypes.c_float, [ctypes.c_uint8]),
@@ -67,6 +74,7 @@ _SIGS = {
     "czo_parallel_max_tasks": (ctypes.c_uint32, []),
     "czo_chunk_bounds": (ctypes.c_uint32, [ctypes.c_size_t, ctypes.c_size_t, vp, ctypes.c_uint32]),
     "czo_cache_replay": (ctypes.c_uint32, [ctypes.c_uint32, vp, ctypes.c_size_t, vp, ctypes.POINTER(CCacheStats)]),
+    "czo_pool_replay": (ctypes.c_int64, [ctypes.c_uint32, vp, ctypes.c_size_t, vp, ctypes.POINTER(CPoolStats)]),
     "czo_chain_layer": (ctypes.c_int, [ctypes.POINTER(CLayer), vp, ctypes.c_size_t, ctypes.c_float, vp, vp, vp]),
     "czo_rms_unit": (None, [vp, vp, ctypes.c_size_t, ctypes.c_float]),
     "czo_exp_audit": (None, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32, vp]),
@@ -230,3 +238,14 @@ def expf(x: np.ndarray) -> np.ndarray:
 
 def fn_ptr(name: str) -> int:
     return ctypes.cast(getattr(lib(), name), vp).value
+
+
+def pool_replay(nslots: int, ops: np.ndarray):
+    """czo_pool_replay over an [n, 4] uint32 op log: (resident at the end or
+    -1, per-op results [n] uint32, stats dict)."""
+    ops = np.ascontiguousarray(ops, np.uint32).reshape(-1, 4)
+    res = np.zeros(len(ops), np.uint32)
+    st = CPoolStats()
+    r = lib().czo_pool_replay(nslots, ops.ctypes.data_as(ctypes.c_void_p), len(ops),
+                              res.ctypes.data_as(ctypes.c_void_p), ctypes.byref(st))
+    return int(r), res, {n: int(getattr(st, n)) for n in POOL_STAT_NAMES}

@@ -32,14 +32,16 @@ NSLOTS = 16  # = E: one layer's whole selection fits at any S; 4 layers x 16 exp
 
 @pytest.fixture(scope="module")
 def pool(gpu):
-    """One pool per context.  The resident side of every comparison runs the
-    streamed tier's three-kernel decode: the one-launch decode is switched
-    off while this module runs and restored after it."""
+    """One pool per context, freed (with its streamed layers) after the
+    module.  The resident side of every comparison runs the streamed tier's
+    three-kernel decode: the one-launch decode is switched off while this
+    module runs and restored after it."""
     moe.stream_pool_init(D, NSLOTS * SLOT)
     hip = _lib.hip()
     prev = hip.colizig_hip_set_fused_decode(0)
     yield True
     hip.colizig_hip_set_fused_decode(prev)
+    moe.stream_pool_free()
 
 
 def _layers(base_res, base_str, nl, seed, zipf=True):

@@ -511,3 +511,88 @@ def test_zipf_bias_skews_popularity(oracle_lib):
     _, idx, _ = O.forward(synth.hidden_states(256, 128, seed=8))
     c = np.bincount(idx.ravel(), minlength=64)
     assert c.max() > 4 * max(np.median(c), 1)
+
+
+def _ops(*rows):
+    return np.array(rows, np.uint32).reshape(-1, 4)
+
+
+GET, PRE, WARM, CLEAR, EPOCH = 1, 2, 3, 4, 0
+HIT = 0x80000000
+
+
+def test_pool_replay_is_the_reference_lru_without_pins(oracle_lib):
+    """With every get in a layer of its own (no pins held across gets) and no
+    prefetch, the pool replay is the reference's per-layer LRU: the same slot
+    for every get as czo_cache_replay on a random trace (whose own policy the
+    hand-worked traces of test_cache_policy pin)."""
+    rng = np.random.default_rng(7)
+    for cap in (1, 3, 8):
+        ids = rng.integers(0, 12, size=200).astype(np.uint32)
+        _, slots, cst = _replay(oracle_lib, cap, ids)
+        ops = []
+        for e in ids:
+            ops += [(EPOCH, 0, 0, 0), (GET, 5, int(e), 0)]
+        r, res, st = oracle_lib.pool_replay(cap, _ops(*ops))
+        gets = res[1::2]
+        assert [int(x) & 0x7fffffff for x in gets] == [int(s) for s in slots]
+        assert (st["hits"], st["misses"], st["evictions"], st["loads"]) == (cst.hits, cst.misses, cst.evictions,
+                                                                          cst.loads)
+        assert int(sum(int(x) >> 31 for x in gets)) == cst.hits
+
+
+def test_pool_replay_pins_and_prefetch(oracle_lib):
+    """Hand-worked: pins of the layer in flight are spared, a prefetch of a
+    resident key is a no-op, one with every slot pinned is dropped, a
+    prefetched slot consumed by a get is a prefetch hit, one evicted unused
+    is wasted; keys of different layers never alias."""
+    r, res, st = oracle_lib.pool_replay(3, _ops(
+        (EPOCH, 0, 0, 0), (GET, 0, 1, 0), (GET, 0, 2, 0),      # slots 0, 1 pinned
+        (PRE, 1, 1, 0),                                          # free slot 2
+        (PRE, 1, 1, 0),                                          # resident: no-op
+        (PRE, 1, 2, 0),                                          # LRU unpinned = slot 2 (just filled): evicts it, wasted
+        (EPOCH, 1, 0, 0), (GET, 1, 2, 0),                        # layer 1 expert 2: hit on slot 2, prefetch hit
+        (GET, 1, 1, 0),                                          # evicted above: miss, victim LRU unpinned = slot 0
+        (GET, 1, 3, 0),                                          # slots 0 and 2 pinned: victim slot 1
+        (PRE, 2, 0, 0),                                          # every slot pinned: dropped
+    ))
+    assert r == 3
+    assert list(res) == [0, 0, 1, 2, 0xfffffffe, 2, 0, 2 | HIT, 0, 1, 0xffffffff]
+    assert st == dict(hits=1, misses=4, loads=6, evictions=3, prefetch_issued=2, prefetch_hits=1, prefetch_wasted=1)
+
+
+def test_pool_replay_warm_clear_and_full_pin(oracle_lib):
+    """Warm fills take free slots only; clear frees every slot (counters
+    kept); a get with every slot pinned is an error (-1)."""
+    r, res, st = oracle_lib.pool_replay(2, _ops((WARM, 0, 4, 0), (WARM, 0, 5, 0), (WARM, 0, 6, 0),
+                                                (EPOCH, 0, 0, 0), (GET, 0, 5, 0), (CLEAR, 0, 0, 0),
+                                                (EPOCH, 0, 0, 0), (GET, 0, 5, 0)))
+    assert list(res) == [0, 1, 0xffffffff, 0, 1 | HIT, 0, 0, 0]
+    assert st["prefetch_issued"] == 2 and st["prefetch_hits"] == 1 and st["misses"] == 1 and r == 1
+    r, _, _ = oracle_lib.pool_replay(1, _ops((EPOCH, 0, 0, 0), (GET, 0, 1, 0), (GET, 0, 2, 0)))
+    assert r == -1
+
+
+def test_pool_replay_invariants(oracle_lib):
+    """The cache invariants (moe.zig:711-741) on random logs: hits + misses =
+    gets; loads = misses + prefetch fills; evictions = loads - resident -
+    (slots freed by clears); resident <= slots."""
+    rng = np.random.default_rng(11)
+    for nslots in (4, 16):
+        ops = []
+        for step in range(60):
+            for layer in range(3):
+                ops.append((EPOCH, layer, 0, 0))
+                for e in rng.choice(10, size=3, replace=False):
+                    ops.append((GET, layer, int(e), 0))
+                for e in rng.choice(10, size=2, replace=False):
+                    ops.append((PRE, (layer + 1) % 3, int(e), 0))
+        r, res, st = oracle_lib.pool_replay(nslots, _ops(*ops))
+        a = _ops(*ops)
+        gets = int((a[:, 0] == GET).sum())
+        fills_pre = int(((a[:, 0] == PRE) & (res < 0xfffffffe)).sum())
+        assert st["hits"] + st["misses"] == gets
+        assert st["loads"] == st["misses"] + fills_pre == st["misses"] + st["prefetch_issued"]
+        assert st["evictions"] == st["loads"] - r
+        assert 0 <= r <= nslots
+        assert st["prefetch_hits"] + st["prefetch_wasted"] <= st["prefetch_issued"]
