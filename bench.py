@@ -69,7 +69,8 @@ def log(msg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 256; 512 for --workload stream, config 5's length)")
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=CONFIG["layers"])
     ap.add_argument("--profile-steps", type=int, default=32)
@@ -88,6 +89,12 @@ def main():
     ap.add_argument("--priors", action="store_true",
                     help="stream: warm the pool from learned priors (.colizig_usage written by an untimed "
                          "previous session of --steps tokens on the same workload) before the timed tokens")
+    ap.add_argument("--predict", type=int, default=2, choices=[0, 1, 2, 3],
+                    help="stream: routing prediction for prefetch (bit 0: next layer from the current layer's "
+                         "router input; bit 1: every later layer from the token's first router input); 0: only "
+                         "the last token's routing")
+    ap.add_argument("--split-slabs", action="store_true",
+                    help="stream: weights and scales in two host slabs (two copies per fill) instead of one packed slab")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
@@ -96,6 +103,8 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.steps is None:
+        args.steps = 512 if args.workload == "stream" else 256
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
@@ -302,7 +311,8 @@ def stream_bench(args) -> None:
     tok/s, the pool's hit rate and the host->HBM rate."""
     from colizig_amd import _lib, moe, synth
     c = dict(CONFIG)
-    c.update(workload="qwen3-30b-a3b-moe-decode-streamed", zipf_s=1.2, drift=0.1, pool_gb=args.pool_gb)
+    c.update(workload="qwen3-30b-a3b-moe-decode-streamed", zipf_s=1.2, drift=0.1, pool_gb=args.pool_gb,
+             routing_prediction=args.predict, host_slabs="split" if args.split_slabs else "packed")
     c["layers"] = args.layers
     H, E, K, I, NL = c["hidden"], c["experts"], c["topk"], c["inter"], c["layers"]
     steps = args.steps
@@ -321,8 +331,16 @@ def stream_bench(args) -> None:
         wb, sb = moe.HostBuffer(E * 3 * mat), moe.HostBuffer(E * 3 * nsc * 4)
         rc = hip.colizig_hip_expert_slab_read(l, wb.ptr, sb.ptr)
         assert rc == 0, _lib.last_error()
-        moe.stream_layer_from_host(l, wb, sb)
-        host.append((wb, sb))
+        if args.split_slabs:
+            moe.stream_layer_from_host(l, wb, sb)
+            host.append((wb, sb))
+        else:
+            hb = moe.host_expert_slab_packed(d, wb.view(np.uint8).reshape(E, -1), sb.view(np.float32).reshape(E, -1))
+            wb.free()
+            sb.free()
+            moe.stream_layer_from_host_packed(l, hb)
+            host.append((hb,))
+    hip.colizig_hip_stream_set_predict(args.predict)
     log(f"expert set in pinned host memory: {NL * E * 3 * mat / 1e9:.1f} GB in {time.time() - t0:.1f}s; "
         f"pool {moe.stream_stats()['slots']} slots")
     # the link on its own: one 1 GiB pinned host->HBM copy
@@ -405,12 +423,13 @@ def stream_bench(args) -> None:
         "config": {**c, "parallelism": "none (1 GPU)", "global_batch": 1, "seq_len": 1},
         "hit_rate": round(hit, 4), "h2d_gbs": round(h2d_gbs, 2), "link_h2d_gbs": round(link_gbs, 2),
         "h2d_link_frac": round(h2d_gbs / link_gbs, 3), "pool": st,
+        "next_layer_prediction_accuracy": round(st["next_correct"] / max(st["next_predicted"], 1), 4),
+        "token_level_prediction_accuracy": round(st["tok_correct"] / max(st["tok_predicted"], 1), 4),
         "roofline": {"bound": "h2d", "achieved": round(h2d_gbs, 2), "peak": round(link_gbs, 2), "unit": "GB/s",
                      "frac": round(h2d_gbs / link_gbs, 3), "traffic": None, "scope": "host->HBM fills"},
     }
     print(json.dumps(line), flush=True)
-    for wb, sb in host:
-        pass  # pinned slabs stay alive until the process ends (the layers point at them)
+    # the pinned slabs in `host` stay allocated until the process ends (the layers point at them)
 
 
 def qwen4_bench(args) -> None:

@@ -149,20 +149,36 @@ struct StreamPool {
     size_t h_idx_cap = 0;
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
     uint32_t seq = 0;
-    // next-layer routing prediction (one token): device scratch of its
-    // routing, its picks in host-coherent memory and their sequence number
-    bool predict_next = true;
+    // routing prediction (one token), bit 0: the next streamed layer's from
+    // the current layer's router input; bit 1: every later streamed layer's
+    // from the chain's first router input.  Device scratch of the predicted
+    // routing, the picks in host-coherent memory and their sequence numbers.
+    int predict_mode = 2;
     float *pred_logits = nullptr, *pred_gates = nullptr, *pred_sgate = nullptr;
     uint32_t *pred_idx = nullptr, *pred_tord = nullptr;
     uint32_t *h_pred = nullptr, *h_pflag = nullptr;
     uint32_t pseq = 0;
-    std::unordered_map<uint32_t, std::vector<uint32_t>> pred_ids;  // layer -> its predicted experts
+    std::unordered_map<uint32_t, std::vector<uint32_t>> pred_ids;  // layer -> its next-layer prediction
     cz::PredStats next_stats;          // next-layer prediction accuracy
+    float *tok_logits = nullptr, *tok_gates = nullptr;
+    uint32_t *tok_idx = nullptr, *tok_tord = nullptr;
+    size_t tok_cap = 0;                // rows (layers) of the token-level buffers
+    const float **tok_ptr_stage = nullptr;  // pinned [2][rows]: routers, biases
+    const float **tok_ptr_dev = nullptr;
+    uint32_t *h_tok = nullptr, *h_tflag = nullptr;
+    uint32_t tseq = 0;
+    std::unordered_map<uint32_t, std::vector<uint32_t>> tok_ids;   // layer -> its token-level prediction
+    cz::PredStats tok_stats;
+    // copy-stream completion per slot: the event recorded after the slot's
+    // latest fill and that fill's sequence number; the compute stream has
+    // waited for every fill up to waited_seq
+    std::vector<hipEvent_t> slot_ev;
+    std::vector<uint64_t> fill_seq;
+    uint64_t fill_counter = 0, waited_seq = 0;
     cz::LastTokenPredictor last_pred{8};
     cz::Scheduler sched{kSchedCapacity};
     bool log_on = false;
     std::vector<uint32_t> log;         // policy ops, 4 words each (op, layer, expert, result)
-    uint32_t fills_pending = 0;        // fills enqueued on the copy stream since the compute stream last waited
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
              prefetch_wasted = 0, bytes_h2d = 0;
@@ -819,7 +835,8 @@ void pool_drop_layer(uint32_t layer);
 int ensure_h_idx(int S);
 struct LayerHost;
 int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, float *out, int rms, float eps,
-                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st);
+                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st,
+                       const std::vector<uint32_t> *later);
 
 LayerHost *find_layer(uint32_t layer) {
     auto it = g.layers.find(layer);
@@ -950,10 +967,13 @@ extern "C" void colizig_cuda_shutdown(void) {
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
     for (void *p : {(void *)P.base, (void *)P.pred_logits, (void *)P.pred_gates, (void *)P.pred_sgate,
-                    (void *)P.pred_idx, (void *)P.pred_tord})
+                    (void *)P.pred_idx, (void *)P.pred_tord, (void *)P.tok_logits, (void *)P.tok_gates,
+                    (void *)P.tok_idx, (void *)P.tok_tord, (void *)P.tok_ptr_dev})
         if (p) (void)hipFree(p);
-    for (void *p : {(void *)P.h_idx, (void *)P.h_flag, (void *)P.h_pred, (void *)P.h_pflag})
+    for (void *p : {(void *)P.h_idx, (void *)P.h_flag, (void *)P.h_pred, (void *)P.h_pflag, (void *)P.h_tok,
+                    (void *)P.h_tflag, (void *)P.tok_ptr_stage})
         if (p) (void)hipHostFree(p);
+    for (hipEvent_t e : P.slot_ev) (void)hipEventDestroy(e);
     if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
     if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
     if (P.copy) (void)hipStreamDestroy(P.copy);
@@ -1404,7 +1424,8 @@ extern "C" int colizig_hip_moe_forward_dev(uint32_t layer, const float *x_dev, i
     if (grouped_ok(L->d, S) && (rc = ensure_work_grouped(L->d, S))) return rc;
     if (L->streamed()) {
         if ((rc = ensure_work_grouped(L->d, S)) || (rc = ensure_h_idx(S))) return rc ? rc : -2;
-        rc = run_streamed_layer(*L, layer, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, 0, pick_stream(stream));
+        rc = run_streamed_layer(*L, layer, x_dev, S, out_dev, 0, 0.0f, nullptr, nullptr, 0, pick_stream(stream),
+                                nullptr);
         if (rc) return rc;
         const size_t kb = (size_t)S * L->d.topk * sizeof(float);
         if (idx_dev) CZ_CHECK(hipMemcpyAsync(idx_dev, g.work.idx, kb, hipMemcpyDeviceToDevice, pick_stream(stream)), -4);
@@ -1522,7 +1543,8 @@ extern "C" int colizig_hip_moe_forward(uint32_t layer, const float *x, int S, fl
     CZ_CHECK(hipMemcpyAsync(g.work.xin, g.h_stage, xb, hipMemcpyHostToDevice, g.stream), -3);
     if (L->streamed()) {
         if ((rc = ensure_work_grouped(L->d, S)) || (rc = ensure_h_idx(S))) return rc ? rc : -2;
-        rc = run_streamed_layer(*L, layer, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, 0, g.stream);
+        rc = run_streamed_layer(*L, layer, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, 0, g.stream,
+                                nullptr);
     } else {
         rc = launch_layer(*L, g.work.xin, S, g.work.out, 0, 0.0f, nullptr, nullptr, nullptr, nullptr, g.stream);
     }
@@ -2000,7 +2022,8 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
         CZ_CHECK(hipMemcpyAsync(dst + P.w_slot, L.host_es + (uint64_t)e * P.s_slot, P.s_slot * sizeof(float),
                                 hipMemcpyHostToDevice, P.copy), -3);
     }
-    P.fills_pending++;
+    CZ_CHECK(hipEventRecord(P.slot_ev[i], P.copy), -4);
+    P.fill_seq[i] = ++P.fill_counter;
     P.bytes_h2d += P.w_slot + P.s_slot * sizeof(float);
     P.loads++;
     P.key[i] = pool_key(layer, e);
@@ -2054,18 +2077,32 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
     if (Ld && sel.size() <= CZ_SEL_ARGS && P.nslots <= 0x10000u && L.d.experts <= 0x10000u) {
         Ld->sel_n = (uint32_t)sel.size();
         for (size_t k = 0; k < sel.size(); ++k) Ld->sel[k] = sel[k] | ((uint32_t)L.slot_map[sel[k]] << 16);
+        // the compute stream waits for the latest fill of these slots only (the
+        // copy stream is in order: that covers the earlier ones); later
+        // prefetches keep filling underneath
+        uint64_t need = P.waited_seq;
+        uint32_t at = 0;
+        for (uint32_t e : sel) {
+            const uint32_t i = (uint32_t)L.slot_map[e];
+            if (P.fill_seq[i] > need) {
+                need = P.fill_seq[i];
+                at = i;
+            }
+        }
+        if (need > P.waited_seq) {
+            CZ_CHECK(hipStreamWaitEvent(st, P.slot_ev[at], 0), -4);
+            P.waited_seq = need;
+        }
     } else {
         // the slot map of this layer: only its selected entries matter (others
-        // may be stale and are never read by this layer's kernels)
+        // may be stale and are never read by this layer's kernels); uploaded
+        // behind every fill so far, which the compute stream then waits for
         memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
         CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
                                 hipMemcpyHostToDevice, P.copy), -3);
-        P.fills_pending++;
-    }
-    if (P.fills_pending) {  // the compute stream waits for everything enqueued on the copy stream
         CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
         CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
-        P.fills_pending = 0;
+        P.waited_seq = P.fill_counter;
     }
     return 0;
 }
@@ -2137,6 +2174,37 @@ int wait_host_seq(const uint32_t *flag, uint32_t seq, hipStream_t st, const char
     }
 }
 
+// Scratch of the token-level prediction for n later layers of E experts.
+int ensure_tok_pred(size_t n, uint32_t E) {
+    StreamPool &P = g.pool;
+    if (!P.h_tflag) {
+        if (hipHostMalloc(&P.h_tflag, 64, hipHostMallocCoherent) != hipSuccess) return -2;
+        __atomic_store_n(P.h_tflag, 0u, __ATOMIC_RELEASE);
+        P.tseq = 0;
+    }
+    if (P.tok_cap >= n) return 0;
+    for (void *p : {(void *)P.tok_logits, (void *)P.tok_gates, (void *)P.tok_idx, (void *)P.tok_tord,
+                    (void *)P.tok_ptr_dev})
+        if (p) (void)hipFree(p);
+    for (void *p : {(void *)P.h_tok, (void *)P.tok_ptr_stage})
+        if (p) (void)hipHostFree(p);
+    P.tok_logits = P.tok_gates = nullptr;
+    P.tok_idx = P.tok_tord = P.h_tok = nullptr;
+    P.tok_ptr_dev = P.tok_ptr_stage = nullptr;
+    P.tok_cap = 0;
+    if (hipMalloc(&P.tok_logits, n * CZ_MAX_E * sizeof(float)) != hipSuccess ||
+        hipMalloc(&P.tok_gates, n * CZ_MAX_K * sizeof(float)) != hipSuccess ||
+        hipMalloc(&P.tok_idx, n * CZ_MAX_K * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&P.tok_tord, n * CZ_MAX_K * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc(&P.tok_ptr_dev, 2 * n * sizeof(float *)) != hipSuccess ||
+        hipHostMalloc(&P.h_tok, n * CZ_MAX_K * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess ||
+        hipHostMalloc(&P.tok_ptr_stage, 2 * n * sizeof(float *), hipHostMallocDefault) != hipSuccess)
+        return -2;
+    (void)E;
+    P.tok_cap = n;
+    return 0;
+}
+
 template <typename F>
 void for_route_groups(uint32_t E, F &&f) {
     switch (cz_route_groups(E)) {
@@ -2160,7 +2228,8 @@ void for_route_groups(uint32_t E, F &&f) {
 // sparing the slots they read.  Scratch (ensure_work + ensure_work_grouped)
 // and the host read-back buffers must be in place.
 int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, float *out, int rms, float eps,
-                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st) {
+                       const float *xres, LayerHost *next, uint32_t next_layer, hipStream_t st,
+                       const std::vector<uint32_t> *later) {
     StreamPool &P = g.pool;
     Work &w = g.work;
     const StepArgs A = step_args(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr);
@@ -2190,7 +2259,7 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         G.host_seq = ++P.seq;
     }
     for_route_groups(A.L.E, [&](auto m) { launch_route_tokens<decltype(m)::value>(G, st); });
-    const bool predict = direct && P.predict_next && next && next->streamed() && next->ready() &&
+    const bool predict = direct && (P.predict_mode & 1) && next && next->streamed() && next->ready() &&
                          next->d.hidden == L.d.hidden && next->d.topk <= CZ_MAX_K;
     if (predict) {
         StepArgs Pn = step_args(*next, G.xn, 1, nullptr, 0, eps, nullptr, nullptr, nullptr, nullptr);
@@ -2214,6 +2283,51 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         G2.host_flag = (uint32_t *)df;
         G2.host_seq = ++P.pseq;
         for_route_groups(next->d.experts, [&](auto m) { launch_route_tokens<decltype(m)::value>(G2, st); });
+    }
+    // every later streamed layer's routing from this router input (the
+    // chain's first): one router launch over the layers, one routing launch
+    // with a row per layer, then the host flag
+    const bool tok_predict = direct && (P.predict_mode & 2) && later && !later->empty() && L.d.hidden % 32 == 0;
+    uint32_t tok_k = 0;
+    if (tok_predict) {
+        const size_t n = later->size();
+        const LayerHost &F0 = *find_layer((*later)[0]);
+        const uint32_t E2 = F0.d.experts;
+        tok_k = F0.d.topk;
+        if (int rc = ensure_tok_pred(n, E2)) return rc;
+        for (size_t i = 0; i < n; ++i) {
+            const LayerHost *Lj = find_layer((*later)[i]);
+            P.tok_ptr_stage[i] = Lj->router;
+            P.tok_ptr_stage[n + i] = Lj->rbias;
+        }
+        CZ_CHECK(hipMemcpyAsync(P.tok_ptr_dev, P.tok_ptr_stage, 2 * n * sizeof(float *), hipMemcpyHostToDevice, st),
+                 -3);
+        RouterLayersArgs R{};
+        R.router = P.tok_ptr_dev;
+        R.bias = P.tok_ptr_dev + n;
+        R.x = G.xn;
+        R.logits = P.tok_logits;
+        R.E = E2;
+        R.H = F0.d.hidden;
+        k_router_layers<<<dim3((E2 + 1) / 2, (uint32_t)n), 64, 0, st>>>(R);
+        GroupArgs G3{};
+        G3.L = F0.dev();
+        G3.S = (int)n;
+        G3.xn = G.xn;
+        G3.logits = P.tok_logits;
+        G3.idx = P.tok_idx;
+        G3.gates = P.tok_gates;
+        G3.sgate = P.pred_sgate;
+        G3.sgate_ready = 1;
+        G3.tok_order = P.tok_tord;
+        G3.usage = nullptr;
+        void *di = nullptr, *df = nullptr;
+        CZ_CHECK(hipHostGetDevicePointer(&di, P.h_tok, 0), -4);
+        CZ_CHECK(hipHostGetDevicePointer(&df, P.h_tflag, 0), -4);
+        G3.host_idx = (uint32_t *)di;
+        G3.host_flag = nullptr;  // published below, once every row is written
+        for_route_groups(E2, [&](auto m) { launch_route_tokens<decltype(m)::value>(G3, st); });
+        k_host_signal<<<1, 64, 0, st>>>((uint32_t *)df, ++P.tseq);
     }
     const size_t nk = (size_t)S * L.d.topk;
     CZ_CHECK(hipGetLastError(), -4);
@@ -2243,6 +2357,11 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
             P.next_stats.score(it->second, P.h_idx, nk);
             P.pred_ids.erase(it);
         }
+        const auto jt = P.tok_ids.find(layer);
+        if (jt != P.tok_ids.end()) {
+            P.tok_stats.score(jt->second, P.h_idx, nk);
+            P.tok_ids.erase(jt);
+        }
         P.last_pred.record(layer, P.h_idx, nk);
     }
     const bool grouped = grouped_ok(L.d, S);
@@ -2264,7 +2383,23 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
         for (uint32_t e : pred) P.sched.submit(cz::ExpertKey{next_layer, e}, cz::kMedium);
     }
     for (uint32_t e : P.last_pred.predict(next_layer)) P.sched.submit(cz::ExpertKey{next_layer, e}, cz::kLow);
-    return pool_service();
+    if ((rc = pool_service())) return rc;
+    if (tok_predict) {  // the later layers' predicted experts, layer by layer
+        if ((rc = wait_host_seq(P.h_tflag, P.tseq, st, "token-level predicted routing read-back"))) return rc;
+        for (size_t i = 0; i < later->size(); ++i) {
+            const uint32_t lj = (*later)[i];
+            const LayerHost *Lj = find_layer(lj);
+            std::vector<uint32_t> &pred = P.tok_ids[lj];
+            pred.clear();
+            for (uint32_t k = 0; k < tok_k; ++k) {
+                const uint32_t e = std::min(P.h_tok[i * tok_k + k], Lj->d.experts - 1);
+                if (std::find(pred.begin(), pred.end(), e) == pred.end()) pred.push_back(e);
+            }
+            for (uint32_t e : pred) P.sched.submit(cz::ExpertKey{lj, e}, cz::kMedium);
+            if ((rc = pool_service())) return rc;
+        }
+    }
+    return 0;
 }
 
 }  // namespace
@@ -2315,6 +2450,13 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
     P.s_slot = s_slot;
     P.slot_bytes = slot_bytes;
     P.nslots = n;
+    while (P.slot_ev.size() < n) {
+        hipEvent_t e = nullptr;
+        CZ_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming), -4);
+        P.slot_ev.push_back(e);
+    }
+    P.fill_seq.assign(n, 0);
+    P.fill_counter = P.waited_seq = 0;
     P.key.assign(n, 0);
     P.used.assign(n, 0);
     P.prefetched.assign(n, 0);
@@ -2357,7 +2499,9 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     P.last_pred.reset();
     P.pred_ids.clear();
     P.next_stats = cz::PredStats{};
-    P.fills_pending = 0;
+    P.tok_ids.clear();
+    P.tok_stats = cz::PredStats{};
+    P.fill_counter = P.waited_seq = 0;
     P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
         P.bytes_h2d = 0;
     P.log.clear();
@@ -2442,12 +2586,30 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
     }
     if (ensure_h_idx(S)) return -2;
     hipStream_t st = g.stream;
+    // the streamed layers after the first one, whose routing the first one
+    // predicts (one token; the same experts, top-k and hidden size)
+    uint32_t first = nlayers;
+    std::vector<uint32_t> later;
+    for (uint32_t l = 0; l < nlayers; ++l) {
+        const LayerHost &L = *find_layer(layer0 + l);
+        if (!L.streamed()) continue;
+        if (first == nlayers) {
+            first = l;
+            continue;
+        }
+        const LayerHost &F = *find_layer(layer0 + first);
+        if (S == 1 && L.d.hidden == F.d.hidden && L.d.experts <= CZ_MAX_E && L.d.topk <= CZ_MAX_K &&
+            (later.empty() || (L.d.experts == find_layer(later[0])->d.experts &&
+                               L.d.topk == find_layer(later[0])->d.topk &&
+                               L.d.norm_topk == find_layer(later[0])->d.norm_topk)))
+            later.push_back(layer0 + l);
+    }
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost &L = *find_layer(layer0 + l);
         LayerHost *next = l + 1 < nlayers ? find_layer(layer0 + l + 1) : nullptr;
-        const int rc = L.streamed()
-                           ? run_streamed_layer(L, layer0 + l, x_dev, S, x_dev, 1, eps, x_dev, next, layer0 + l + 1, st)
-                           : launch_layer(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, st);
+        const int rc = L.streamed() ? run_streamed_layer(L, layer0 + l, x_dev, S, x_dev, 1, eps, x_dev, next,
+                                                         layer0 + l + 1, st, l == first ? &later : nullptr)
+                                    : launch_layer(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, st);
         if (rc) return rc;
     }
     return 0;
@@ -2527,7 +2689,7 @@ extern "C" int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32
         ++warmed;
     }
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
-    P.fills_pending = 0;
+    P.waited_seq = P.fill_counter;  // every fill is complete
     return (int)warmed;
 }
 
@@ -2545,9 +2707,10 @@ extern "C" int colizig_hip_stream_evict_all(void) {
         P.prefetched[i] = 0;
     }
     P.where.clear();
-    P.fills_pending = 0;
+    P.waited_seq = P.fill_counter;  // every fill is complete
     P.sched.clear();
     P.pred_ids.clear();
+    P.tok_ids.clear();
     P.last_pred.reset();
     pool_log(kOpClear, 0, 0, 0);
     for (auto &kv : g.layers)
@@ -2561,22 +2724,24 @@ extern "C" int colizig_hip_stream_stats(uint64_t *out, int n) {
     const StreamPool &P = g.pool;
     const cz::SchedStats &s = P.sched.stats();
     const cz::PredStats &lt = P.last_pred.stats();
-    const uint64_t v[23] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
+    const uint64_t v[25] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
                             P.prefetch_wasted, P.bytes_h2d, P.nslots, (uint64_t)P.where.size(),
                             P.next_stats.predicted, P.next_stats.correct, lt.predicted, lt.correct,
                             s.submitted, s.deduped, s.upgraded, s.rejected_full, s.serviced[0], s.serviced[1],
-                            s.serviced[2], s.cancelled, s.queue_peak};
+                            s.serviced[2], s.cancelled, s.queue_peak, P.tok_stats.predicted, P.tok_stats.correct};
     if (!out || n < 1) return -1;
-    for (int i = 0; i < n && i < 23; ++i) out[i] = v[i];
+    for (int i = 0; i < n && i < 25; ++i) out[i] = v[i];
     return 0;
 }
 
-// Next-layer routing prediction on or off (returns the previous setting).
-extern "C" int colizig_hip_stream_set_predict(int enable) {
+// Routing prediction mode (bit 0 next layer, bit 1 every later layer from
+// the chain's first router input); returns the previous mode.
+extern "C" int colizig_hip_stream_set_predict(int mode) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    const int prev = g.pool.predict_next ? 1 : 0;
-    g.pool.predict_next = enable != 0;
+    if (mode < 0 || mode > 3) return -1;
+    const int prev = g.pool.predict_mode;
+    g.pool.predict_mode = mode;
     return prev;
 }
 

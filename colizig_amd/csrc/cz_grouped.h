@@ -64,7 +64,8 @@ struct GroupArgs {
     const float *xres;         // [S][H] nullable
     float *out;                // [S][H]
     // S = 1 routing read back by the host without a copy: the picks go to
-    // host_idx (host memory), then host_seq to host_flag (system scope)
+    // host_idx (host memory), then host_seq to host_flag (system scope; a
+    // null flag: a later kernel publishes it)
     uint32_t *host_idx;        // nullable
     uint32_t *host_flag;
     uint32_t host_seq;
@@ -124,7 +125,8 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
     if (G.host_idx) {  // one token (one wave): picks to host memory, then the flag
         if (lane < L.K) G.host_idx[(uint64_t)t * L.K + o_pos] = o_id;
         __threadfence_system();
-        if (lane == 0) __hip_atomic_store(G.host_flag, G.host_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (lane == 0 && G.host_flag)
+            __hip_atomic_store(G.host_flag, G.host_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     if (split) {
         _Float16 *xh = G.xh + (uint64_t)t * L.H, *xl = G.xl + (uint64_t)t * L.H;

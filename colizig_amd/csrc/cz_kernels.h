@@ -335,6 +335,43 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
     }
 }
 
+// Router logits of several layers for one token (the streaming tier's
+// prediction of later layers' routing from one router input): logits[l][e]
+// = router_l[e] . x (+ bias_l[e]) in the decode router's dotF32 order (so
+// the same input gives the same logits); one wave per two experts of one
+// layer (blockIdx.y).  H % 32 == 0.
+struct RouterLayersArgs {
+    const float *const *router;  // [n] router of each layer, [E][H]
+    const float *const *bias;    // [n] its bias [E], or null
+    const float *x;              // [H]
+    float *logits;               // [n][E]
+    uint32_t E, H;
+};
+
+__global__ __launch_bounds__(64) void k_router_layers(RouterLayersArgs A) {
+    const uint32_t l = blockIdx.y, lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31;
+    const uint32_t e = blockIdx.x * 2 + half, ec = min(e, A.E - 1);
+    const float *wr = A.router[l] + (uint64_t)ec * A.H + j;
+    const float *xr = A.x + j;
+    float acc = 0.0f;
+    const uint32_t n = A.H / 32;
+#pragma unroll 16
+    for (uint32_t i = 0; i < n; ++i) acc = __builtin_fmaf(xr[32 * i], wr[32 * i], acc);
+    float lg = cz_router_combine(acc, j, half * 32);
+    const float *b = A.bias[l];
+    if (b) lg = lg + b[ec];
+    if (j == 0 && e < A.E) A.logits[(uint64_t)l * A.E + e] = lg;
+}
+
+// Publishes `seq` to a host-memory flag after everything before it on the
+// stream (system-scope release).
+__global__ void k_host_signal(uint32_t *flag, uint32_t seq) {
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 // Many-token router input (S > 1, rms = 1): one wave per token writes xn =
 // rms(x) (rmsnorm.zig:32-40 with a unit weight: the f64 sum of the squares,
 // cz_rms_inv), and, when xh / xl are given, xn split into f16 hi + lo (the

@@ -285,18 +285,22 @@ int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts
 int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32_t experts, const uint64_t *counts);
 int colizig_hip_stream_evict_all(void);
 
-/* Pool counters, out[0..n) (n <= 23): hits, misses, loads, evictions,
+/* Pool counters, out[0..n) (n <= 25): hits, misses, loads, evictions,
  * prefetch_issued, prefetch_hits, prefetch_wasted (CacheStats,
  * moe.zig:121-139), bytes_h2d, slots, resident entries; next-layer
  * prediction: ids predicted, ids correct; last-token prediction: predicted,
  * correct (predict.zig:19-27); scheduler (io.zig:38-52): submitted, deduped,
  * upgraded, rejected_full, serviced HIGH / MEDIUM / LOW, cancelled,
- * queue_peak. */
+ * queue_peak; token-level prediction: predicted, correct. */
 int colizig_hip_stream_stats(uint64_t *out, int n);
 
-/* Next-layer routing prediction on (default) or off; returns the previous
- * setting. */
-int colizig_hip_stream_set_predict(int enable);
+/* Routing prediction for prefetch at one token: bit 0, the next streamed
+ * layer's routing from the current layer's router input (its router and
+ * routing kernels run once more on that input); bit 1, every later streamed
+ * layer's from the chain's first streamed layer's router input (one router
+ * launch over those layers, one routing launch).  Default 2.  Returns the
+ * previous mode, -1 for a mode outside 0..3. */
+int colizig_hip_stream_set_predict(int mode);
 
 /* Op log of the pool's policy (test hook).  colizig_hip_stream_log(1) clears
  * and starts it, (0) stops it.  colizig_hip_stream_log_read copies up to

@@ -3,7 +3,8 @@
 pinned host memory (packed slabs, one copy per fill), an HBM pool of 64
 slots (the working set is 512 experts), routing Zipf(1.2)-skewed over a
 seeded permutation per layer with 10% of the experts swapping ranks after
-every step, 32 decode steps at batch 1 with the next-layer prediction on.
+every step, 32 decode steps at batch 1 with both routing predictions on
+(next layer, and every later layer from the token's first router input).
 
 Against the oracle:
 - every layer's demand gets (its picks, in pick order, repeats dropped)
@@ -80,7 +81,7 @@ def c5(gpu, oracle_lib):
         hosts.append(host)
         packs.append(packed)
         layers.append(L)
-    prev = hip.colizig_hip_stream_set_predict(1)
+    prev = hip.colizig_hip_stream_set_predict(3)  # both predictions: the op log covers both kinds of prefetch
     yield dict(d=d, hosts=hosts, packs=packs, layers=layers, ranks=ranks, rng=rng)
     hip.colizig_hip_stream_set_predict(prev)
     hip.colizig_hip_stream_log(0)
@@ -146,6 +147,7 @@ def test_c5_stream_vs_oracle_chain_and_policy(c5, oracle_lib):
     assert lib_st["resident"] == r
     assert lib_st["hits"] + lib_st["misses"] == sum(len(s) for _, s in picks_o)
     assert lib_st["next_predicted"] == (STEPS * NL - STEPS) * K  # every layer but the first of each step
+    assert lib_st["tok_predicted"] == (STEPS * NL - STEPS) * K
     acc = lib_st["next_correct"] / lib_st["next_predicted"]
     say(f"  x rel L2 <= {worst:.2e}; {len(ops)} pool ops replayed; hits {lib_st['hits']} misses "
         f"{lib_st['misses']} evictions {lib_st['evictions']}; prefetch issued {lib_st['prefetch_issued']} hits "
