@@ -320,7 +320,12 @@ def stream_bench(args) -> None:
     log(f"device: {name}")
     hip = _lib.hip()
     d = moe.dims(H, E, K, I, 0, True)
-    moe.stream_pool_init(d, int(args.pool_gb * 1e9))
+    # the HBM plan for a 16 GB expert budget (budget.plan restated for HBM):
+    # every layer streams through one pool of that many expert slots
+    plan = moe.plan_hbm(d, NL, moe.plan_hbm(d, NL, 1 << 40)["fixed_resident"] + int(args.pool_gb * 1e9))
+    assert plan["fits"] and not plan["all_resident"], plan
+    moe.stream_pool_init(d, plan["expert_bytes"])
+    c["hbm_plan"] = {k: plan[k] for k in ("pool_slots", "expert_cap", "ladder_cap", "fixed_resident", "total")}
     t0 = time.time()
     mat, nsc = I * H, nblk(I) * nblk(H)
     zero_router = np.zeros((E, H), np.float32)

@@ -36,6 +36,26 @@ class Dims(ctypes.Structure):
         return self.shared_inter != 0
 
 
+class HbmPlan(ctypes.Structure):
+    """`colizig_hbm_plan` - budget.plan's Plan (src/runtime/budget.zig:66-90) for HBM."""
+
+    _fields_ = [
+        ("hbm_budget", ctypes.c_uint64),
+        ("per_expert_bytes", ctypes.c_uint64),
+        ("per_layer_fixed", ctypes.c_uint64),
+        ("scratch", ctypes.c_uint64),
+        ("fixed_resident", ctypes.c_uint64),
+        ("expert_bytes", ctypes.c_uint64),
+        ("total", ctypes.c_uint64),
+        ("all_resident", ctypes.c_uint32),
+        ("pool_slots", ctypes.c_uint32),
+        ("expert_cap", ctypes.c_uint32),
+        ("ladder_cap", ctypes.c_uint32),
+        ("fits", ctypes.c_uint32),
+        ("reason", ctypes.c_char * 128),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     # the existing backend ABI (src/backend/gpu.zig:20-34)
@@ -86,6 +106,8 @@ SIGNATURES = {
     "colizig_hip_stream_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int, ctypes.c_float]),
     "colizig_hip_stream_stats": (ctypes.c_int, [c_u64p, ctypes.c_int]),
     "colizig_hip_stream_pool_free": (ctypes.c_int, []),
+    "colizig_hip_plan_hbm": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,
+                                            ctypes.POINTER(HbmPlan)]),
     "colizig_hip_layer_stream_from_host_packed": (ctypes.c_int, [ctypes.c_uint32, vp]),
     "colizig_hip_stream_set_predict": (ctypes.c_int, [ctypes.c_int]),
     "colizig_hip_stream_log": (ctypes.c_int, [ctypes.c_int]),

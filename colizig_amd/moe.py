@@ -350,6 +350,19 @@ def stream_layer_from_host_packed(layer: int, hb: HostBuffer) -> None:
            _lib.hip().colizig_hip_layer_stream_from_host_packed(layer, hb.ptr))
 
 
+def plan_hbm(d: Dims, layers: int, hbm_budget: int = 0, max_tokens: int = 1) -> dict:
+    """budget.plan (src/runtime/budget.zig:184-264) for one GPU's HBM: the
+    resident bytes, and whether every expert stays resident or how many
+    expert slots the streaming pool gets (hbm_budget 0: the device's free
+    memory less an eighth; needs init)."""
+    p = _lib.HbmPlan()
+    _check("colizig_hip_plan_hbm", _lib.hip().colizig_hip_plan_hbm(ctypes.byref(d), layers, hbm_budget, max_tokens,
+                                                                     ctypes.byref(p)))
+    out = {name: getattr(p, name) for name, _ in _lib.HbmPlan._fields_}
+    out["reason"] = p.reason.decode()
+    return out
+
+
 def stream_pool_free() -> None:
     _check("colizig_hip_stream_pool_free", _lib.hip().colizig_hip_stream_pool_free())
 

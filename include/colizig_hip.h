@@ -339,6 +339,33 @@ int colizig_hip_predictor_record(int64_t h, uint32_t layer, const uint32_t *ids,
 int colizig_hip_predictor_predict(int64_t h, uint32_t layer, uint32_t *out, uint32_t max);
 int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint64_t *correct);
 
+/* ---- HBM plan (budget.plan, src/runtime/budget.zig:59-264, for HBM) ------
+ * Where a model's MoE bytes go on one GPU: every layer keeps its router (f32
+ * [E][H]), its shared expert and sigmoid gate, its routed-selection counters
+ * and slot map resident; the routed experts are either all resident (when
+ * they fit) or streamed through one HBM pool of expert slots shared by every
+ * layer (the reference's per-layer cache cap, as one budget).  Host code:
+ * with hbm_budget = 0 the budget is the device's free memory less an eighth
+ * (the colizig_cuda_set_vram_budget clamp, needs colizig_cuda_init);
+ * max_tokens sizes the forward's scratch. */
+typedef struct colizig_hbm_plan {
+    uint64_t hbm_budget;         /* bytes the plan may use */
+    uint64_t per_expert_bytes;   /* one routed expert: weights + scales (one pool slot) */
+    uint64_t per_layer_fixed;    /* router + shared expert + sh_gate + counters + slot map */
+    uint64_t scratch;            /* the forward's scratch for max_tokens tokens */
+    uint64_t fixed_resident;     /* layers * per_layer_fixed + scratch */
+    uint64_t expert_bytes;       /* experts resident, or the pool */
+    uint64_t total;              /* fixed_resident + expert_bytes */
+    uint32_t all_resident;       /* 1: every expert resident, no streaming */
+    uint32_t pool_slots;         /* streamed: expert slots of the pool */
+    uint32_t expert_cap;         /* streamed: pool_slots / layers (the average cap per layer) */
+    uint32_t ladder_cap;         /* the largest cap_ladder entry <= expert_cap (budget.zig:62), 0 below it */
+    uint32_t fits;               /* 0: not even top-k slots fit after the fixed bytes */
+    char reason[128];            /* "" when it fits */
+} colizig_hbm_plan;
+int colizig_hip_plan_hbm(const colizig_dims *dims, uint32_t layers, uint64_t hbm_budget, uint32_t max_tokens,
+                         colizig_hbm_plan *out);
+
 /* Pinned host memory for the host expert slabs. */
 void *colizig_hip_host_alloc(uint64_t bytes);
 void colizig_hip_host_free(void *p);
