@@ -55,6 +55,11 @@ struct LayerHost {
     float *shg = nullptr;
     float *rbias = nullptr;  // optional router bias [E]
     unsigned long long *usage = nullptr;  // [E] routed-selection counters (ExpertUsage row)
+    uint16_t *router_bf16 = nullptr;      // BF16 router [E][H] (NativeMatrix bf16); `router` is then null
+    // a NativeMatrix shared expert (f32 or BF16 rows, moe.zig:300-303,
+    // 467-479), evaluated by its own GEMVs after the routed experts
+    int shn_dtype = -1;                   // 0 f32, 1 bf16, -1 none (FP8 or no shared expert)
+    void *shn_gate = nullptr, *shn_up = nullptr, *shn_down = nullptr;
     // streamed from host memory: experts live in pinned host memory (two
     // slabs in the ew/es layout, or one packed slab of [weights | scales] per
     // expert) and in slots of the HBM expert pool while cached
@@ -101,6 +106,14 @@ struct LayerHost {
         L.router_bias = rbias;
         L.slot_map = slot_map_dev;
         L.usage = usage;
+        L.router_bf16 = router_bf16;
+        if (shn_dtype >= 0) {  // the routed-expert kernels see no shared expert
+            L.SI = 0;
+            L.nbSI = 0;
+            L.sw = nullptr;
+            L.ss = nullptr;
+            L.sh_gate = nullptr;
+        }
         return L;
     }
 };
@@ -110,6 +123,8 @@ struct LayerHost {
 struct Work {
     float *xin = nullptr, *out = nullptr, *xn = nullptr, *logits = nullptr, *gates = nullptr, *sgate = nullptr;
     float *h = nullptr, *hs = nullptr;
+    float *ng = nullptr, *nu = nullptr, *no = nullptr, *nsg = nullptr;  // NativeMatrix shared expert
+    size_t cap_ng = 0, cap_nu = 0, cap_no = 0, cap_nsg = 0;
     uint32_t *idx = nullptr;
     size_t cap_xin = 0, cap_out = 0, cap_xn = 0, cap_logits = 0, cap_idx = 0, cap_gates = 0, cap_sgate = 0,
            cap_h = 0, cap_hs = 0;
@@ -291,7 +306,9 @@ int ensure_work(const colizig_dims &d, int S) {
         grow(&w.xn, &w.cap_xn, s * d.hidden) || grow(&w.logits, &w.cap_logits, s * d.experts) ||
         grow(&w.idx, &w.cap_idx, s * d.topk) || grow(&w.gates, &w.cap_gates, s * d.topk) ||
         grow(&w.sgate, &w.cap_sgate, s) || grow(&w.h, &w.cap_h, s * d.topk * (size_t)d.inter) ||
-        grow(&w.hs, &w.cap_hs, std::max<size_t>(1, s * d.shared_inter))) {
+        grow(&w.hs, &w.cap_hs, std::max<size_t>(1, s * d.shared_inter)) ||
+        (d.shared_inter && (grow(&w.ng, &w.cap_ng, s * d.shared_inter) || grow(&w.nu, &w.cap_nu, s * d.shared_inter) ||
+                            grow(&w.no, &w.cap_no, s * d.hidden) || grow(&w.nsg, &w.cap_nsg, s)))) {
         snprintf(g_err, sizeof g_err, "scratch allocation failed (S=%d)", S);
         return -2;
     }
@@ -338,7 +355,8 @@ void free_layer(LayerHost &L) {
         for (void *p : {(void *)L.ew, (void *)L.es})
             if (p) (void)hipFree(p);
     for (void *p : {(void *)L.router, (void *)L.sw, (void *)L.ss, (void *)L.shg, (void *)L.rbias,
-                    (void *)L.slot_map_dev, (void *)L.usage})
+                    (void *)L.slot_map_dev, (void *)L.usage, (void *)L.router_bf16, L.shn_gate, L.shn_up,
+                    L.shn_down})
         if (p) (void)hipFree(p);
     if (L.slot_map_stage) (void)hipHostFree(L.slot_map_stage);
     L = LayerHost{};
@@ -377,8 +395,54 @@ bool rms_rows_write_sgate(const StepArgs &A) {
     return A.rms && A.S >= kGroupedMinTokens && L.H % 256 == 0 && L.SI != 0 && (L.H / 4 + 255) / 256 <= 8;
 }
 
+// y[S][O] = x[S][I] . W^T for NativeMatrix rows (f32: dotF32; BF16: dotBf16,
+// tensors.zig:114-119), bit for bit.
+template <typename T>
+void launch_gemv_native(float *y, const float *x, const T *w, int S, int I, int O, hipStream_t st) {
+    constexpr int WPB = 8;
+    const dim3 grid((O + 2 * WPB - 1) / (2 * WPB)), blk(64 * WPB);
+    switch ((I % 32) ? 0 : I / 32) {
+        case 8: k_gemv_native<8, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        case 16: k_gemv_native<16, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        case 32: k_gemv_native<32, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        case 64: k_gemv_native<64, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        case 96: k_gemv_native<96, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        case 128: k_gemv_native<128, WPB, T><<<grid, blk, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)O); return;
+        default:
+            k_gemv_native_any<T><<<(O + 1) / 2, 64, 0, st>>>(y, x, w, (uint32_t)S, (uint32_t)I, (uint32_t)O);
+            return;
+    }
+}
+
+// A BF16 router (NativeMatrix bf16, tensors.zig:114-119): rms rows first when
+// asked (the same bits as the f32 router kernels' staging), then dotBf16 rows
+// and the bias add.
+void launch_router_bf16(const StepArgs &A, hipStream_t st) {
+    const LayerDev &L = A.L;
+    const float *xin = A.x;
+    if (A.rms) {
+        switch (L.H % 256 ? 0u : (L.H / 4 + 255) / 256) {
+            case 1: k_rms_rows_wg<1><<<A.S, 256, 0, st>>>(A); break;
+            case 2: k_rms_rows_wg<2><<<A.S, 256, 0, st>>>(A); break;
+            case 4: k_rms_rows_wg<4><<<A.S, 256, 0, st>>>(A); break;
+            case 8: k_rms_rows_wg<8><<<A.S, 256, 0, st>>>(A); break;
+            default: k_rms_rows<<<(A.S + 3) / 4, 256, 0, st>>>(A); break;
+        }
+        xin = A.xn;
+    }
+    launch_gemv_native<uint16_t>(A.logits, xin, L.router_bf16, A.S, (int)L.H, (int)L.E, st);
+    if (L.router_bias) {
+        const uint64_t n = (uint64_t)A.S * L.E;
+        k_add_bias<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(A.logits, L.router_bias, (uint32_t)A.S, L.E);
+    }
+}
+
 void launch_router(const StepArgs &A, hipStream_t st) {
     const LayerDev &L = A.L;
+    if (L.router_bf16) {
+        launch_router_bf16(A, st);
+        return;
+    }
     if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
         if (A.rms) {
             switch ((L.H / 4 + 255) / 256) {  // 128-bit words per thread
@@ -568,6 +632,48 @@ void launch_route_tokens(const GroupArgs &G, hipStream_t st) {
     k_route_tokens<M><<<(G.S + 3) / 4, 256, 0, st>>>(G);
 }
 
+// A NativeMatrix shared expert (moe.zig:467-479): from the MoE input xn,
+// before the routed kernels (which may write over x): gate and up rows (f32
+// or BF16, dotF32 / dotBf16 order), h = silu(g) * u, the down rows and the
+// sigmoid gate, kept in scratch; then, after the routed experts' combine,
+// out += sgate * shared.
+int launch_shared_native_pre(const LayerHost &Lh, const float *xn, int S, hipStream_t st) {
+    Work &w = g.work;
+    const int H = (int)Lh.d.hidden, SI = (int)Lh.d.shared_inter;
+    if (Lh.shn_dtype == 1) {
+        launch_gemv_native<uint16_t>(w.ng, xn, (const uint16_t *)Lh.shn_gate, S, H, SI, st);
+        launch_gemv_native<uint16_t>(w.nu, xn, (const uint16_t *)Lh.shn_up, S, H, SI, st);
+    } else {
+        launch_gemv_native<float>(w.ng, xn, (const float *)Lh.shn_gate, S, H, SI, st);
+        launch_gemv_native<float>(w.nu, xn, (const float *)Lh.shn_up, S, H, SI, st);
+    }
+    const uint64_t n = (uint64_t)S * SI;
+    k_swiglu_native<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(w.ng, w.nu, n);
+    if (Lh.shn_dtype == 1)
+        launch_gemv_native<uint16_t>(w.no, w.ng, (const uint16_t *)Lh.shn_down, S, SI, H, st);
+    else
+        launch_gemv_native<float>(w.no, w.ng, (const float *)Lh.shn_down, S, SI, H, st);
+    k_shared_gate_native<<<S, 64, 0, st>>>(w.nsg, xn, Lh.shg, (uint32_t)H);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "shared expert launch: %s", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
+int launch_shared_native_add(const LayerHost &Lh, float *out, int S, hipStream_t st) {
+    const uint64_t n = (uint64_t)S * Lh.d.hidden;
+    k_shared_add_native<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(out, g.work.no, g.work.nsg, (uint32_t)S,
+                                                                    Lh.d.hidden);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "shared expert launch: %s", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
 int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
                    float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
     StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
@@ -578,6 +684,9 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         A.xl = w.xl;
     }
     launch_router(A, st);
+    if (Lh.shn_dtype >= 0) {
+        if (int rc = launch_shared_native_pre(Lh, rms ? w.xn : x, S, st)) return rc;
+    }
     GroupArgs G{};
     G.L = L;
     G.S = S;
@@ -684,6 +793,9 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     const uint32_t qd = L.SI ? (mts * (L.H / cd) + 7) / 8 * 8 : 0u;
     k_gg<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
     k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
+    if (Lh.shn_dtype >= 0) {
+        if (int rc = launch_shared_native_add(Lh, out, S, st)) return rc;
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_err, sizeof g_err, "grouped launch: %s", hipGetErrorString(e));
@@ -701,7 +813,8 @@ LayerHost *find_layer(uint32_t layer);
 bool fused_ok(const LayerHost &L, int S) {
     const colizig_dims &d = L.d;
     if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG) return false;
-    if (d.shared_inter != 0 || d.experts > 128 || d.topk > CZ_MAX_K || d.inter % CZ_BLOCK) return false;
+    if (d.shared_inter != 0 || d.experts > 128 || d.topk > CZ_MAX_K || d.inter % CZ_BLOCK || L.router_bf16)
+        return false;
     if (d.hidden != 512 && d.hidden != 1024 && d.hidden != 2048) return false;
     const uint64_t ki = (uint64_t)d.topk * d.inter;
     if (ki % 1024) return false;
@@ -828,7 +941,13 @@ int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms
                  float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
     if (grouped_ok(Lh.d, S))
         return launch_grouped(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace, st);
-    return launch_step(step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace), st);
+    const StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
+    if (Lh.shn_dtype < 0) return launch_step(A, st);
+    int rc = launch_step(A, st, kRouter);
+    if (!rc) rc = launch_shared_native_pre(Lh, rms ? g.work.xn : x, S, st);
+    if (!rc) rc = launch_step(A, st, kUp | kDown);
+    if (!rc) rc = launch_shared_native_add(Lh, out, S, st);
+    return rc;
 }
 
 void pool_drop_layer(uint32_t layer);
@@ -957,7 +1076,8 @@ extern "C" void colizig_cuda_shutdown(void) {
                     (void *)w.sgate, (void *)w.h, (void *)w.hs, (void *)w.idx, (void *)w.counts, (void *)w.offsets,
                     (void *)w.sorted_slot, (void *)w.slot_pos, (void *)w.tok_order, (void *)w.tile_expert,
                     (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os, (void *)w.xh, (void *)w.xl,
-                    (void *)w.hh, (void *)w.hl, (void *)w.hsh, (void *)w.hsl})
+                    (void *)w.hh, (void *)w.hl, (void *)w.hsh, (void *)w.hsl, (void *)w.ng, (void *)w.nu,
+                    (void *)w.no, (void *)w.nsg})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     for (void *p : {(void *)g.fused.r, (void *)g.fused.p, (void *)g.fused.zero, (void *)g.fused.lgx,
@@ -1168,13 +1288,6 @@ extern "C" int colizig_hip_matrix_load_bf16(uint64_t key, const uint16_t *w, int
     return 0;
 }
 
-template <int NS>
-void launch_gemv_bf16(float *y, const float *x, const Slot &sl, int S, int O, hipStream_t st) {
-    constexpr int WPB = 8;
-    k_gemv_bf16<NS, WPB><<<(O + 2 * WPB - 1) / (2 * WPB), 64 * WPB, 0, st>>>(y, x, (const uint16_t *)sl.w,
-                                                                              (uint32_t)S, (uint32_t)O);
-}
-
 extern "C" int colizig_hip_matmul_bf16_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key,
                                            void *stream) {
     CsrGuard csr;
@@ -1194,17 +1307,7 @@ extern "C" int colizig_hip_matmul_bf16_dev(float *y_dev, const float *x_dev, int
     sl.clock = ++g.lru;
     g.hits++;
     const hipStream_t st = pick_stream(stream);
-    switch ((I % 32) ? 0 : I / 32) {
-        case 8: launch_gemv_bf16<8>(y_dev, x_dev, sl, S, O, st); break;
-        case 16: launch_gemv_bf16<16>(y_dev, x_dev, sl, S, O, st); break;
-        case 32: launch_gemv_bf16<32>(y_dev, x_dev, sl, S, O, st); break;
-        case 64: launch_gemv_bf16<64>(y_dev, x_dev, sl, S, O, st); break;
-        case 96: launch_gemv_bf16<96>(y_dev, x_dev, sl, S, O, st); break;
-        case 128: launch_gemv_bf16<128>(y_dev, x_dev, sl, S, O, st); break;
-        default:
-            snprintf(g_err, sizeof g_err, "matmul_bf16_dev: row width %d (supported: 32 x {8,16,32,64,96,128})", I);
-            return -1;
-    }
+    launch_gemv_native<uint16_t>(y_dev, x_dev, (const uint16_t *)sl.w, S, I, O, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_err, sizeof g_err, "matmul_bf16_dev launch: %s", hipGetErrorString(e));
@@ -1375,6 +1478,17 @@ extern "C" int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char 
         return -1;
     const uint64_t mb = (uint64_t)L->d.shared_inter * L->d.hidden;
     const uint64_t nsc = (uint64_t)nblk(L->d.shared_inter) * nblk(L->d.hidden);
+    (void)hipStreamSynchronize(g.stream);
+    if (L->shn_dtype >= 0) {  // a NativeMatrix shared expert is replaced
+        for (void *p : {L->shn_gate, L->shn_up, L->shn_down})
+            if (p) (void)hipFree(p);
+        L->shn_gate = L->shn_up = L->shn_down = nullptr;
+        L->shn_dtype = -1;
+        L->gen = ++g.layer_gen;
+    }
+    if (!L->sw && (hipMalloc(&L->sw, L->sw_bytes()) != hipSuccess ||
+                   hipMalloc(&L->ss, L->ss_floats() * sizeof(float)) != hipSuccess))
+        return -2;
     CZ_CHECK(hipMemcpyAsync(L->sw, gate_w, mb, hipMemcpyHostToDevice, g.stream), -3);
     CZ_CHECK(hipMemcpyAsync(L->sw + mb, up_w, mb, hipMemcpyHostToDevice, g.stream), -3);
     CZ_CHECK(hipMemcpyAsync(L->sw + 2 * mb, down_w, mb, hipMemcpyHostToDevice, g.stream), -3);
@@ -1384,6 +1498,63 @@ extern "C" int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char 
     CZ_CHECK(hipMemcpyAsync(L->shg, sh_gate, (size_t)L->d.hidden * 4, hipMemcpyHostToDevice, g.stream), -3);
     CZ_CHECK(hipStreamSynchronize(g.stream), -3);
     L->shared_set = true;
+    return 0;
+}
+
+// A NativeMatrix shared expert (moe.zig:300-303, 316-325: the reference keeps
+// shared_expert.{gate,up,down}_proj as f32 or BF16 rows and evaluates them
+// with dotF32 / dotBf16): gate, up [SI][H], down [H][SI], dtype 0 f32, 1 BF16
+// (raw bits); sh_gate [H] f32.  Replaces a block-FP8 shared expert.
+extern "C" int colizig_hip_layer_set_shared_native(uint32_t layer, int dtype, const void *gate, const void *up,
+                                                   const void *down, const float *sh_gate) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || L->d.shared_inter == 0 || (dtype != 0 && dtype != 1) || !gate || !up || !down ||
+        !sh_gate)
+        return -1;
+    const size_t es = dtype == 1 ? 2 : 4, mb = (size_t)L->d.shared_inter * L->d.hidden * es;
+    (void)hipStreamSynchronize(g.stream);
+    for (void *p : {L->shn_gate, L->shn_up, L->shn_down, (void *)L->sw, (void *)L->ss})
+        if (p) (void)hipFree(p);
+    L->shn_gate = L->shn_up = L->shn_down = nullptr;
+    L->sw = nullptr;
+    L->ss = nullptr;
+    L->shn_dtype = -1;
+    L->shared_set = false;
+    L->gen = ++g.layer_gen;
+    if (hipMalloc(&L->shn_gate, mb) != hipSuccess || hipMalloc(&L->shn_up, mb) != hipSuccess ||
+        hipMalloc(&L->shn_down, mb) != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "layer %u: shared expert allocation failed", layer);
+        return -2;
+    }
+    CZ_CHECK(hipMemcpy(L->shn_gate, gate, mb, hipMemcpyHostToDevice), -3);
+    CZ_CHECK(hipMemcpy(L->shn_up, up, mb, hipMemcpyHostToDevice), -3);
+    CZ_CHECK(hipMemcpy(L->shn_down, down, mb, hipMemcpyHostToDevice), -3);
+    CZ_CHECK(hipMemcpy(L->shg, sh_gate, (size_t)L->d.hidden * 4, hipMemcpyHostToDevice), -3);
+    L->shn_dtype = dtype;
+    L->shared_set = true;
+    return 0;
+}
+
+// A BF16 router (NativeMatrix bf16, tensors.zig:114-119; raw bits [E][H])
+// in place of the f32 one: logits in dotBf16's order (matmul.zig:84-110).
+extern "C" int colizig_hip_layer_set_router_bf16(uint32_t layer, const uint16_t *router) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    LayerHost *L = find_layer(layer);
+    if (!g.inited || !L || !router) return -1;
+    if (L->streamed() && g.pool.on) (void)hipStreamSynchronize(g.pool.copy);
+    (void)hipStreamSynchronize(g.stream);
+    const size_t n = (size_t)L->d.experts * L->d.hidden;
+    if (!L->router_bf16 && hipMalloc(&L->router_bf16, n * 2) != hipSuccess) {
+        L->router_bf16 = nullptr;
+        return -2;
+    }
+    CZ_CHECK(hipMemcpy(L->router_bf16, router, n * 2, hipMemcpyHostToDevice), -3);
+    if (L->router) (void)hipFree(L->router);
+    L->router = nullptr;
+    L->gen = ++g.layer_gen;
     return 0;
 }
 
@@ -1497,6 +1668,11 @@ extern "C" int colizig_hip_moe_forward_dev_noalloc(uint32_t layer, const float *
     if (grouped_ok(L->d, S)) {
         snprintf(g_err, sizeof g_err, "no-alloc forward: S=%d takes the grouped regime (S >= %d), which this "
                  "entry point does not serve", S, kGroupedMinTokens);
+        return -1;
+    }
+    if (L->shn_dtype >= 0) {
+        snprintf(g_err, sizeof g_err, "no-alloc forward: layer %u has a NativeMatrix shared expert, which this "
+                 "entry point does not serve", layer);
         return -1;
     }
     size_t off[7];
@@ -1719,8 +1895,9 @@ extern "C" int colizig_hip_layer_synth(uint32_t layer, uint64_t seed, float std_
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     LayerHost *L = find_layer(layer);
     if (!g.inited || !L) return -1;
-    if (L->streamed()) {
-        snprintf(g_err, sizeof g_err, "layer %u streams from host memory", layer);
+    if (L->streamed() || !L->router || L->shn_dtype >= 0 || (L->d.shared_inter && !L->sw)) {
+        snprintf(g_err, sizeof g_err, "layer %u streams from host memory or holds NativeMatrix weights: synthesis "
+                 "writes the f32 router and block-FP8 experts of a resident layer", layer);
         return -1;
     }
     const colizig_dims &d = L->d;
@@ -1790,7 +1967,17 @@ extern "C" int colizig_hip_router_read(uint32_t layer, float *router) {
     LayerHost *L = find_layer(layer);
     if (!g.inited || !L || !router) return -1;
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
-    CZ_CHECK(hipMemcpy(router, L->router, (size_t)L->d.experts * L->d.hidden * 4, hipMemcpyDeviceToHost), -5);
+    const size_t n = (size_t)L->d.experts * L->d.hidden;
+    if (L->router_bf16) {  // widened (exact)
+        std::vector<uint16_t> b(n);
+        CZ_CHECK(hipMemcpy(b.data(), L->router_bf16, n * 2, hipMemcpyDeviceToHost), -5);
+        for (size_t i = 0; i < n; ++i) {
+            const uint32_t u = (uint32_t)b[i] << 16;
+            memcpy(router + i, &u, 4);
+        }
+        return 0;
+    }
+    CZ_CHECK(hipMemcpy(router, L->router, n * 4, hipMemcpyDeviceToHost), -5);
     return 0;
 }
 
@@ -1799,7 +1986,7 @@ extern "C" int colizig_hip_shared_read(uint32_t layer, unsigned char *gate_w, fl
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     LayerHost *L = find_layer(layer);
-    if (!g.inited || !L || L->d.shared_inter == 0) return -1;
+    if (!g.inited || !L || L->d.shared_inter == 0 || !L->sw) return -1;  // none, or NativeMatrix rows
     const uint64_t mb = (uint64_t)L->d.shared_inter * L->d.hidden;
     const uint64_t nsc = (uint64_t)nblk(L->d.shared_inter) * nblk(L->d.hidden);
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
@@ -2368,8 +2555,13 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     StepArgs A2 = A;  // the decode kernels can take the slots in their arguments
     int rc = stream_resident(L, layer, sel, st, grouped ? nullptr : &A2.L);
     if (rc) return rc;
-    rc = grouped ? launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st)
-                 : launch_step(A2, st, kUp | kDown);
+    if (grouped) {
+        rc = launch_grouped(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr, st);
+    } else {
+        if (L.shn_dtype >= 0 && (rc = launch_shared_native_pre(L, G.xn, S, st))) return rc;
+        rc = launch_step(A2, st, kUp | kDown);
+        if (!rc && L.shn_dtype >= 0) rc = launch_shared_native_add(L, out, S, st);
+    }
     if (rc) return rc;
     if (!next || !next->streamed()) return 0;
     if (predict) {
@@ -2598,7 +2790,8 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
             continue;
         }
         const LayerHost &F = *find_layer(layer0 + first);
-        if (S == 1 && L.d.hidden == F.d.hidden && L.d.experts <= CZ_MAX_E && L.d.topk <= CZ_MAX_K &&
+        if (S == 1 && !L.router_bf16 && L.d.hidden == F.d.hidden && L.d.experts <= CZ_MAX_E &&
+            L.d.topk <= CZ_MAX_K &&
             (later.empty() || (L.d.experts == find_layer(later[0])->d.experts &&
                                L.d.topk == find_layer(later[0])->d.topk &&
                                L.d.norm_topk == find_layer(later[0])->d.norm_topk)))

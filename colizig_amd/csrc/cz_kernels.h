@@ -47,6 +47,7 @@ struct LayerDev {
     const int32_t *slot_map;   // [E] HBM pool slot of each expert (layers streamed from
                                // host memory; ew/es then point at the pool), or null
     unsigned long long *usage; // [E] routed-selection counters (bumpUsage, moe.zig:428-432), or null
+    const uint16_t *router_bf16;  // [E][H] BF16 router (NativeMatrix bf16), or null: `router` is f32
 };
 
 // bumpUsage (moe.zig:428-432): one count per pick of a token (all K of them,
@@ -967,18 +968,21 @@ __global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const f
 }
 
 // ---------------------------------------------------------------------------
-// BF16 GEMV on device-resident activations (lm_head and other BF16
-// NativeMatrix rows, matmul.zig:84-110 dotBf16): y[S][O] with each dot in
-// dotBf16's order, which is dotF32's (matmul.zig:60-82) on the widened
-// weights: half-wave per row as the router kernel (lane j = chain j over
-// elements j + 32i, then cz_router_combine), so results are bit-identical to
-// the reference's.  WPB waves per workgroup (2 WPB rows) share the token rows
-// staged in LDS, ST at a time; I = 32 NS.  Rows past O are read as row O - 1
-// and not stored (every wave reaches every barrier).
+// NativeMatrix GEMV on device-resident activations (tensors.zig:114-119: f32
+// rows through dotF32, matmul.zig:60-82; BF16 rows through dotBf16,
+// matmul.zig:84-110, which is dotF32's order on the widened weights): y[S][O]
+// with every dot in that order: half-wave per row as the router kernel (lane
+// j = chain j over elements j + 32i, then cz_router_combine), so results are
+// bit-identical to the reference's.  WPB waves per workgroup (2 WPB rows)
+// share the token rows staged in LDS, ST at a time; I = 32 NS.  Rows past O
+// are read as row O - 1 and not stored (every wave reaches every barrier).
 // ---------------------------------------------------------------------------
-template <int NS, int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_gemv_bf16(float *__restrict__ y, const float *__restrict__ x,
-                                                        const uint16_t *__restrict__ w, uint32_t S, uint32_t O) {
+__device__ inline float cz_widen(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ inline float cz_widen(float f) { return f; }
+
+template <int NS, int WPB, typename T>
+__global__ __launch_bounds__(64 * WPB) void k_gemv_native(float *__restrict__ y, const float *__restrict__ x,
+                                                          const T *__restrict__ w, uint32_t S, uint32_t O) {
     constexpr uint32_t I = 32 * NS, I4 = I / 4, NT = 64 * WPB;
     constexpr uint32_t ST = I >= 8192 ? 1 : 8192 / I < 4 ? 8192 / I : 4;  // tokens per pass: <= 32 KiB of LDS
     constexpr uint32_t NQ = (ST * I4 + NT - 1) / NT;
@@ -988,9 +992,9 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_bf16(float *__restrict__ y, c
     const uint32_t r = blockIdx.x * 2 * WPB + 2 * wave + half;
     const uint32_t row = min(r, O - 1);
     float wv[NS];
-    const uint16_t *wr = w + (uint64_t)row * I + j;
+    const T *wr = w + (uint64_t)row * I + j;
 #pragma unroll
-    for (int i = 0; i < NS; ++i) wv[i] = __builtin_bit_cast(float, (uint32_t)wr[32 * i] << 16);
+    for (int i = 0; i < NS; ++i) wv[i] = cz_widen(wr[32 * i]);
     constexpr int CB = NS < 32 ? NS : 32;
     for (uint32_t t0 = 0; t0 < S; t0 += ST) {
         const uint32_t n4 = min(ST, S - t0) * I4;
@@ -1017,6 +1021,60 @@ __global__ __launch_bounds__(64 * WPB) void k_gemv_bf16(float *__restrict__ y, c
             if (j == 0 && r < O) y[(uint64_t)(t0 + t) * O + r] = lg;
         }
         __syncthreads();  // these tokens' readers are done before the next pass stores
+    }
+}
+
+// Any row width: the same dot order (dotF32's tails: 8-wide steps on lanes
+// j < 8, then a scalar FMA tail), the weights read per token.  One wave per
+// two rows.
+template <typename T>
+__global__ __launch_bounds__(64) void k_gemv_native_any(float *__restrict__ y, const float *__restrict__ x,
+                                                        const T *__restrict__ w, uint32_t S, uint32_t I, uint32_t O) {
+    const uint32_t lane = threadIdx.x & 63, half = lane >> 5, j = lane & 31, hb = half * 32;
+    const uint32_t r = blockIdx.x * 2 + half, row = min(r, O - 1);
+    const T *wr = w + (uint64_t)row * I;
+    for (uint32_t t = 0; t < S; ++t) {
+        const float *a = x + (uint64_t)t * I;
+        float acc = 0.0f;
+        uint32_t i = 0;
+        for (; i + 32 <= I; i += 32) acc = __builtin_fmaf(a[i + j], cz_widen(wr[i + j]), acc);
+        for (; i + 8 <= I; i += 8)
+            if (j < 8) acc = __builtin_fmaf(a[i + j], cz_widen(wr[i + j]), acc);
+        float sum = cz_router_combine(acc, j, hb);
+        for (; i < I; ++i) sum = __builtin_fmaf(a[i], cz_widen(wr[i]), sum);
+        if (j == 0 && r < O) y[(uint64_t)t * O + r] = sum;
+    }
+}
+
+// logits[t][e] += bias[e] (the router kernels' one f32 add after the dot)
+__global__ void k_add_bias(float *__restrict__ logits, const float *__restrict__ bias, uint32_t S, uint32_t E) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (uint64_t)S * E) logits[i] = logits[i] + bias[i % E];
+}
+
+// A NativeMatrix shared expert (moe.zig:467-479): h = silu(g) * u in place
+// of g, f32 (activation.zig:18-20 with the correctly rounded exp).
+__global__ void k_swiglu_native(float *__restrict__ g, const float *__restrict__ u, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) g[i] = cz_silu(g[i]) * u[i];
+}
+
+// sgate_t = sigmoid(sum_d xn_t[d] * sh_gate[d]) (serial order, moe.zig:475-477),
+// one wave per token.
+__global__ __launch_bounds__(64) void k_shared_gate_native(float *__restrict__ sgate, const float *__restrict__ xn,
+                                                           const float *__restrict__ sh_gate, uint32_t H) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63;
+    const float d = cz_sgate_dot(xn + (uint64_t)t * H, sh_gate, H, lane);
+    if (lane == 0) sgate[t] = cz_sigmoid(d);
+}
+
+// out[t][i] += sgate_t * shared[t][i] (moe.zig:478)
+__global__ void k_shared_add_native(float *__restrict__ out, const float *__restrict__ shared,
+                                    const float *__restrict__ sgate, uint32_t S, uint32_t H) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (uint64_t)S * H) {
+        const float prod = sgate[i / H] * shared[i];
+        out[i] = out[i] + prod;
     }
 }
 

@@ -5,15 +5,17 @@ Tensor names follow the reference's lookup (weights.zig:204-207): a suffix
 such as ``layers.{l}.mlp.experts.{e}.gate_proj.weight`` is looked up as
 ``<prefix>.<suffix>`` first, then bare.  Per layer:
 
-- router ``layers.{l}.mlp.gate.weight`` [E, H], F32 or BF16 (widened to f32,
-  exactly);
+- router ``layers.{l}.mlp.gate.weight`` [E, H], F32 or BF16, kept in its
+  own dtype in HBM (NativeMatrix.load, tensors.zig:74-94: other dtypes are
+  refused);
 - experts ``layers.{l}.mlp.experts.{e}.{gate,up,down}_proj.weight`` (F8_E4M3
   bytes, [I, H] / [I, H] / [H, I]) with ``.weight_scale_inv`` (F32, one per
   128 x 128 block), the multiplier the reference applies to the E4M3 value
   (fp8.zig:105);
 - a shared expert, when the layer has one: ``shared_expert.{gate,up,down}_proj``
-  in the same block-FP8 form and ``shared_expert_gate.weight`` [H] (F32 or
-  BF16).
+  as F32 or BF16 NativeMatrix rows (the reference's form, moe.zig:316-325), or
+  in the routed experts' block-FP8 form, and ``shared_expert_gate.weight`` [H]
+  (F32 or BF16).
 
 The safetensors container (safetensors.zig:126-237): an 8-byte little-endian
 header length, a JSON header {name: {dtype, shape, data_offsets}}, then the
@@ -144,6 +146,19 @@ class Checkpoint:
             return a.astype(np.float32)
         raise CheckpointError(f"{suffix}: dtype {t.dtype}, expected F32, BF16 or F16")
 
+    def native(self, suffix: str, shape: tuple) -> np.ndarray:
+        """NativeMatrix.load (tensors.zig:74-94): an F32 matrix as float32 or a
+        BF16 one as its uint16 bits; any other dtype is refused."""
+        t, a = self.raw(suffix)
+        if t.dtype not in ("F32", "BF16"):
+            raise CheckpointError(f"{suffix}: dtype {t.dtype}, expected F32 or BF16")
+        if t.shape != shape:
+            raise CheckpointError(f"{suffix}: shape {t.shape}, expected {shape}")
+        return np.ascontiguousarray(a)
+
+    def dtype(self, suffix: str) -> str:
+        return self.raw(suffix)[0].dtype
+
     def fp8_matrix(self, stem: str, rows: int, cols: int) -> tuple[np.ndarray, np.ndarray]:
         """`stem.weight` (F8_E4M3 [rows, cols]) and `stem.weight_scale_inv`
         (F32 [ceil(rows/128), ceil(cols/128)]), as Fp8Matrix.load takes them."""
@@ -165,23 +180,34 @@ def load_layer(ckpt: Checkpoint, layer: int, d: moe.Dims, layer_id: int | None =
     (default: the same number), experts uploaded to their HBM slots."""
     H, E, I, SI = d.hidden, d.experts, d.inter, d.shared_inter
     p = f"layers.{layer}.mlp"
-    router = ckpt.f32(f"{p}.gate.weight")
-    if router.shape != (E, H):
-        raise CheckpointError(f"{p}.gate.weight: shape {router.shape}, expected {(E, H)}")
-    L = moe.Layer.load(layer if layer_id is None else layer_id, d, router)
+    router = ckpt.native(f"{p}.gate.weight", (E, H))
+    lid = layer if layer_id is None else layer_id
+    if router.dtype == np.uint16:  # BF16 rows stay BF16 (dotBf16 logits)
+        L = moe.Layer.load(lid, d, np.zeros((E, H), np.float32))
+        L.set_router_bf16(router)
+    else:
+        L = moe.Layer.load(lid, d, router)
     for e in range(E):
         gw, gs = ckpt.fp8_matrix(f"{p}.experts.{e}.gate_proj", I, H)
         uw, us = ckpt.fp8_matrix(f"{p}.experts.{e}.up_proj", I, H)
         dw, ds = ckpt.fp8_matrix(f"{p}.experts.{e}.down_proj", H, I)
         L.load_expert(e, gw, gs, uw, us, dw, ds)
     if SI:
-        gw, gs = ckpt.fp8_matrix(f"{p}.shared_expert.gate_proj", SI, H)
-        uw, us = ckpt.fp8_matrix(f"{p}.shared_expert.up_proj", SI, H)
-        dw, ds = ckpt.fp8_matrix(f"{p}.shared_expert.down_proj", H, SI)
         g = ckpt.f32(f"{p}.shared_expert_gate.weight").reshape(-1)
         if g.shape != (H,):
             raise CheckpointError(f"{p}.shared_expert_gate.weight: {g.size} values, expected {H}")
-        L.set_shared(gw, gs, uw, us, dw, ds, g)
+        if ckpt.dtype(f"{p}.shared_expert.gate_proj.weight") == "F8_E4M3":
+            gw, gs = ckpt.fp8_matrix(f"{p}.shared_expert.gate_proj", SI, H)
+            uw, us = ckpt.fp8_matrix(f"{p}.shared_expert.up_proj", SI, H)
+            dw, ds = ckpt.fp8_matrix(f"{p}.shared_expert.down_proj", H, SI)
+            L.set_shared(gw, gs, uw, us, dw, ds, g)
+        else:  # NativeMatrix rows (moe.zig:316-325), one dtype for the three
+            gm = ckpt.native(f"{p}.shared_expert.gate_proj.weight", (SI, H))
+            um = ckpt.native(f"{p}.shared_expert.up_proj.weight", (SI, H))
+            dm = ckpt.native(f"{p}.shared_expert.down_proj.weight", (H, SI))
+            if not (gm.dtype == um.dtype == dm.dtype):
+                raise CheckpointError(f"{p}.shared_expert: gate/up/down of different dtypes")
+            L.set_shared_native(gm, um, dm, g)
     return L
 
 

@@ -184,6 +184,25 @@ class Layer:
         _check("colizig_hip_layer_set_shared",
                _lib.hip().colizig_hip_layer_set_shared(self.layer, *[_p(a) for a in arrs]))
 
+    def set_router_bf16(self, bits: np.ndarray) -> None:
+        """A BF16 router (NativeMatrix bf16, tensors.zig:65-120) as raw bits
+        [E][H]; logits in dotBf16's order (matmul.zig:84-110)."""
+        b = np.ascontiguousarray(bits, dtype=np.uint16)
+        assert b.shape == (self.d.experts, self.d.hidden)
+        _check("colizig_hip_layer_set_router_bf16", _lib.hip().colizig_hip_layer_set_router_bf16(self.layer, _p(b)))
+
+    def set_shared_native(self, gate: np.ndarray, up: np.ndarray, down: np.ndarray, sh_gate: np.ndarray) -> None:
+        """A NativeMatrix shared expert (moe.zig:300-303, 316-325): gate, up
+        [SI][H] and down [H][SI] as f32 or BF16 bits (uint16), sh_gate [H]."""
+        H, SI = self.d.hidden, self.d.shared_inter
+        bf16 = np.asarray(gate).dtype == np.uint16
+        t = np.uint16 if bf16 else np.float32
+        g, u, dn = (np.ascontiguousarray(m, dtype=t) for m in (gate, up, down))
+        assert g.shape == (SI, H) and u.shape == (SI, H) and dn.shape == (H, SI)
+        sg = np.ascontiguousarray(sh_gate, dtype=np.float32)
+        _check("colizig_hip_layer_set_shared_native", _lib.hip().colizig_hip_layer_set_shared_native(
+            self.layer, 1 if bf16 else 0, _p(g), _p(u), _p(dn), _p(sg)))
+
     def set_router_bias(self, bias: np.ndarray | None) -> None:
         """Optional per-expert logit bias (workload shaping; None clears it)."""
         b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
@@ -235,12 +254,19 @@ class Layer:
 def register_layer(layer: int, host: dict) -> Layer:
     """Registers a host-built layer (colizig_amd.synth.make_layer layout)."""
     d = Dims(**host["dims"])
-    L = Layer.load(layer, d, host["router"])
+    router = np.asarray(host["router"])
+    bf16_router = router.dtype == np.uint16  # BF16 bits: a NativeMatrix bf16 router
+    L = Layer.load(layer, d, np.zeros((d.experts, d.hidden), np.float32) if bf16_router else router)
+    if bf16_router:
+        L.set_router_bf16(router)
     for e, ex in enumerate(host["experts"]):
         L.load_expert(e, ex["gate_w"], ex["gate_s"], ex["up_w"], ex["up_s"], ex["down_w"], ex["down_s"])
     if host.get("shared") is not None:
         s = host["shared"]
-        L.set_shared(s["gate_w"], s["gate_s"], s["up_w"], s["up_s"], s["down_w"], s["down_s"], s["sh_gate"])
+        if "native" in s:
+            L.set_shared_native(s["gate"], s["up"], s["down"], s["sh_gate"])
+        else:
+            L.set_shared(s["gate_w"], s["gate_s"], s["up_w"], s["up_s"], s["down_w"], s["down_s"], s["sh_gate"])
     if host.get("router_bias") is not None:
         L.set_router_bias(host["router_bias"])
     return L

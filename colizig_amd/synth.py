@@ -106,3 +106,30 @@ def zipf_router_bias(E: int, s: float, seed: int) -> np.ndarray:
     ranks[rng.permutation(E)] = np.arange(1, E + 1, dtype=np.float64)
     lp = -s * np.log(ranks)
     return (lp - lp.mean()).astype(np.float32)
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round f32 values to BF16 (nearest, ties to even) as uint16 bits."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def with_native(host: dict, seed: int, router_bf16: bool = True, shared: str | None = None,
+                std_w: float = 0.02) -> dict:
+    """A make_layer host with NativeMatrix weights (tensors.zig:65-120): the
+    router rounded to BF16 bits, and/or (shared = "f32" or "bf16") a shared
+    expert of f32 or BF16 rows drawn N(0, std_w) with an f32 sh_gate."""
+    out = dict(host)
+    if router_bf16:
+        out["router"] = f32_to_bf16_bits(host["router"])
+    if shared:
+        d = host["dims"]
+        H, SI = d["hidden"], d["shared_inter"]
+        assert SI, "the dims have no shared expert"
+        rng = np.random.default_rng(seed)
+        mats = [rng.normal(0.0, std_w, size=s).astype(np.float32) for s in ((SI, H), (SI, H), (H, SI))]
+        if shared == "bf16":
+            mats = [f32_to_bf16_bits(m) for m in mats]
+        sg = host["shared"]["sh_gate"] if host.get("shared") else rng.normal(0.0, 0.02, size=(H,)).astype(np.float32)
+        out["shared"] = dict(native=shared, gate=mats[0], up=mats[1], down=mats[2], sh_gate=sg)
+    return out

@@ -127,6 +127,21 @@ int colizig_hip_expert_load(uint32_t layer, uint32_t expert, const unsigned char
 
 /* Shared expert of a layer (moe.zig:300-303, 319-325), block-FP8:
  * gate/up [SI,H], down [H,SI], sh_gate[H] f32 (shared_expert_gate.weight). */
+/* NativeMatrix weights (src/model/tensors.zig:65-120), as the reference
+ * loads a router or shared expert stored in f32 or BF16.
+ * colizig_hip_layer_set_router_bf16: the router as BF16 bits [E][H] (replaces
+ * the f32 one; logits in dotBf16's order, matmul.zig:84-110, bit for bit).
+ * colizig_hip_layer_set_shared_native: the shared expert's gate, up [SI][H]
+ * and down [H][SI] rows as f32 (dtype 0) or BF16 bits (dtype 1), evaluated
+ * with dotF32 / dotBf16 rows (moe.zig:300-303, 316-325, 467-479), plus
+ * sh_gate [H] f32; replaces a block-FP8 shared expert.  Such a layer runs
+ * the three-kernel decode and its shared-expert GEMVs (not the one-launch
+ * decode) and is not served by colizig_hip_moe_forward_dev_noalloc.
+ * -1 bad args / no shared expert in the dims; -2 alloc; -3 copy. */
+int colizig_hip_layer_set_router_bf16(uint32_t layer, const uint16_t *router);
+int colizig_hip_layer_set_shared_native(uint32_t layer, int dtype, const void *gate, const void *up,
+                                        const void *down, const float *sh_gate);
+
 int colizig_hip_layer_set_shared(uint32_t layer, const unsigned char *gate_w, const float *gate_s,
                                  const unsigned char *up_w, const float *up_s, const unsigned char *down_w,
                                  const float *down_s, const float *sh_gate);

@@ -625,10 +625,18 @@ static void czo_add_shared(const czo_layer *L, const float *xs, float *ys, float
     const czo_dims *d = &L->d;
     if (d->shared_inter == 0) return;
     const uint32_t H = d->hidden, SI = d->shared_inter;
-    czo_matmul_fp8(sg, xs, L->sh_gate_proj.w, L->sh_gate_proj.s, 1, H, SI);
-    czo_matmul_fp8(su, xs, L->sh_up_proj.w, L->sh_up_proj.s, 1, H, SI);
+    if (L->sh_native_gate) { /* NativeMatrix.matmul (tensors.zig:114-119) */
+        czo_matmul_f32(sg, xs, L->sh_native_gate, 1, H, SI);
+        czo_matmul_f32(su, xs, L->sh_native_up, 1, H, SI);
+    } else {
+        czo_matmul_fp8(sg, xs, L->sh_gate_proj.w, L->sh_gate_proj.s, 1, H, SI);
+        czo_matmul_fp8(su, xs, L->sh_up_proj.w, L->sh_up_proj.s, 1, H, SI);
+    }
     for (uint32_t j = 0; j < SI; ++j) sh[j] = czo_silu(sg[j]) * su[j];
-    czo_matmul_fp8(shared, sh, L->sh_down_proj.w, L->sh_down_proj.s, 1, SI, H);
+    if (L->sh_native_down)
+        czo_matmul_f32(shared, sh, L->sh_native_down, 1, SI, H);
+    else
+        czo_matmul_fp8(shared, sh, L->sh_down_proj.w, L->sh_down_proj.s, 1, SI, H);
     float sgate = 0;
     for (uint32_t dd = 0; dd < H; ++dd) {
         const float prod = xs[dd] * L->sh_gate[dd];

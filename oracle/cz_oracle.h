@@ -67,6 +67,12 @@ typedef struct czo_layer {
     czo_fp8mat sh_down_proj;   /* [hidden, shared_inter] */
     const float *sh_gate;      /* [hidden] f32 */
     const float *router_bias;  /* [experts] added to each logit, or NULL (the reference: none) */
+    /* A NativeMatrix shared expert (moe.zig:300-303: f32 rows, or BF16 rows
+     * widened exactly, since dotBf16 is dotF32's order on the widened values,
+     * matmul.zig:60-110): when set, used instead of the block-FP8 one. */
+    const float *sh_native_gate;  /* [shared_inter, hidden] */
+    const float *sh_native_up;    /* [shared_inter, hidden] */
+    const float *sh_native_down;  /* [hidden, shared_inter] */
 } czo_layer;
 
 /* ---- fp8.zig ---------------------------------------------------------- */

@@ -33,7 +33,17 @@ class CExpert(ctypes.Structure):
 class CLayer(ctypes.Structure):
     _fields_ = [("d", CDims), ("router", vp), ("experts", ctypes.POINTER(CExpert)),
                 ("sh_gate_proj", CMat), ("sh_up_proj", CMat), ("sh_down_proj", CMat), ("sh_gate", vp),
-                ("router_bias", vp)]
+                ("router_bias", vp), ("sh_native_gate", vp), ("sh_native_up", vp), ("sh_native_down", vp)]
+
+
+def widen_bf16(bits: np.ndarray) -> np.ndarray:
+    """BF16 bit patterns -> f32, exactly (bf16 is the top half of an f32)."""
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def native_f32(m: np.ndarray) -> np.ndarray:
+    """A NativeMatrix's values as f32: BF16 bits (uint16) widened, f32 as is."""
+    return widen_bf16(m) if m.dtype == np.uint16 else np.ascontiguousarray(m, dtype=np.float32)
 
 
 class CCacheStats(ctypes.Structure):
@@ -118,7 +128,8 @@ class OracleLayer:
         d = host["dims"]
         self.host = host
         self._keep = []
-        self.router = np.ascontiguousarray(host["router"], dtype=np.float32)
+        # an f32 router, or BF16 bits: dotBf16 is dotF32 on the widened values (matmul.zig:60-110)
+        self.router = native_f32(np.asarray(host["router"]))
         exs = (CExpert * d["experts"])()
         for e, ex in enumerate(host["experts"]):
             arr = {k: np.ascontiguousarray(v) for k, v in ex.items()}
@@ -130,8 +141,17 @@ class OracleLayer:
         L.d = CDims(d["hidden"], d["experts"], d["topk"], d["inter"], d["shared_inter"], d["norm_topk"])
         L.router = _p(self.router)
         L.experts = exs
-        if host.get("shared") is not None:
-            s = {k: np.ascontiguousarray(v) for k, v in host["shared"].items()}
+        sh = host.get("shared")
+        if sh is not None and "native" in sh:  # NativeMatrix rows (f32 or BF16 bits)
+            s = {k: native_f32(np.asarray(sh[k])) for k in ("gate", "up", "down")}
+            s["sh_gate"] = np.ascontiguousarray(sh["sh_gate"], dtype=np.float32)
+            self._keep.append(s)
+            L.sh_native_gate = _p(s["gate"])
+            L.sh_native_up = _p(s["up"])
+            L.sh_native_down = _p(s["down"])
+            L.sh_gate = _p(s["sh_gate"])
+        elif sh is not None:
+            s = {k: np.ascontiguousarray(v) for k, v in sh.items()}
             self._keep.append(s)
             L.sh_gate_proj = _mat(s["gate_w"], s["gate_s"])
             L.sh_up_proj = _mat(s["up_w"], s["up_s"])

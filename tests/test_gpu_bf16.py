@@ -23,7 +23,11 @@ def _bf16(rng, O, I):
     return (rng.normal(0.0, 0.02, size=(O, I)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
 
 
-@pytest.mark.parametrize("O,I,S", [(1000, 2048, 1), (4099, 2048, 3), (512, 4096, 2), (33, 256, 5), (96, 3072, 1)])
+# the last three widths are not a multiple of 256 x 32 tiles: the any-width
+# kernel, dotBf16's 8-wide steps and scalar tail included (200 = 6*32 + 8,
+# 45 = 32 + 8 + 5)
+@pytest.mark.parametrize("O,I,S", [(1000, 2048, 1), (4099, 2048, 3), (512, 4096, 2), (33, 256, 5), (96, 3072, 1),
+                                   (8, 200, 3), (17, 45, 2), (64, 384, 1)])
 def test_bf16_rows_bit_exact(gpu, oracle_lib, O, I, S):
     say(f"bf16 gemv {O}x{I} S={S}")
     moe.set_vram_budget(1 << 30)
@@ -48,8 +52,8 @@ def test_bf16_rows_bit_exact(gpu, oracle_lib, O, I, S):
 
 
 def test_bf16_key_type_checks(gpu):
-    """A BF16 key is not an FP8 matrix and the reverse (-1); an unsupported
-    row width (-1); a missing key (-7)."""
+    """A BF16 key is not an FP8 matrix and the reverse (-1); a call with
+    another shape than the resident one (-1); a missing key (-7)."""
     say("bf16 key checks")
     hip = _lib.hip()
     moe.set_vram_budget(1 << 30)
@@ -63,7 +67,8 @@ def test_bf16_key_type_checks(gpu):
         assert hip.colizig_hip_matmul_bf16_dev(yb.ptr, xb.ptr, 1, 2048, 64, kb, None) == 0
         kw = moe.Fp8Matrix.expert_key(41, 1, 3)
         moe.matrix_load_bf16(kw, _bf16(rng, 8, 200))
-        assert hip.colizig_hip_matmul_bf16_dev(yb.ptr, xb.ptr, 1, 200, 8, kw, None) == -1
+        assert hip.colizig_hip_matmul_bf16_dev(yb.ptr, xb.ptr, 1, 200, 8, kw, None) == 0
+        assert hip.colizig_hip_matmul_bf16_dev(yb.ptr, xb.ptr, 1, 192, 8, kw, None) == -1
         assert hip.colizig_hip_matmul_bf16_dev(yb.ptr, xb.ptr, 1, 2048, 64, 0xBADBAD, None) == -7
         assert hip.colizig_hip_sync() == 0
     finally:
