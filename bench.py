@@ -77,14 +77,16 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=4)
-    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead", "dropin"],
+                    default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
                          "512 tokens with Zipf(1.1) routing skew (grouped regime); stream: batch-1 decode "
                          "with the expert set in pinned host memory and a 16 GB HBM expert pool; qwen4: "
                          "Qwen4-Exp-style stack (36 layers, H4096, E512 top-10, shared 4096) at batch 1 and 32; "
                          "attn: the FP8 attention projections q/k/v/o of 48 Qwen3-30B-A3B layers at batch 1 "
                          "(keyed device GEMV); lmhead: the BF16 lm_head GEMV (151936 x 2048) at batch 1, "
-                         "dotBf16 order")
+                         "dotBf16 order; dropin: the unchanged engine's per-matmul calls (colizig_cuda_matmul_fp8 "
+                         "on host buffers, keyed hits) at the Qwen3-30B-A3B expert and attention shapes")
     ap.add_argument("--pool-gb", type=float, default=16.0, help="stream: HBM expert pool cap (GB)")
     ap.add_argument("--priors", action="store_true",
                     help="stream: warm the pool from learned priors (.colizig_usage written by an untimed "
@@ -122,6 +124,9 @@ def main():
         return
     if args.workload == "lmhead":
         lmhead_bench(args)
+        return
+    if args.workload == "dropin":
+        dropin_bench(args)
         return
 
     from colizig_amd import _lib, moe
@@ -619,6 +624,72 @@ def lmhead_bench(args) -> None:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": LMHEAD_TRAFFIC_BYTES, "scope": "one launch"},
     }))
+
+
+def dropin_bench(args) -> None:
+    """The drop-in path as the unchanged engine drives it: Fp8Matrix.matmul ->
+    fp8.matmulFp8Keyed -> gpu.matmulFp8 -> colizig_cuda_matmul_fp8 (host
+    pointers, synchronous, keyed; fp8.zig:165-194, gpu.zig:175-190), once per
+    expert projection: per layer and token 3 x top-k = 24 expert calls at
+    batch 1 (gate and up 768 x 2048, down 2048 x 768), plus the four FP8
+    attention projections (q 4096 x 2048, k and v 512 x 2048, o 2048 x 4096).
+    Every key is resident (a warm-up call uploads it), so each call is a
+    keyed hit: x in, y out over PCIe, one kernel, one synchronisation.
+    Reports the mean time per call of each shape and the implied MoE + attention
+    projection time of a 48-layer token (the engine's own CPU work - router,
+    attention, norms - not included)."""
+    from colizig_amd import _lib, moe, synth
+    name = moe.init()
+    log(f"device: {name}")
+    hip = _lib.hip()
+    moe.set_vram_budget(8 << 30)
+    rng = np.random.default_rng(11)
+    H, I, K = 2048, 768, 8
+    shapes = {"expert_gate_up": (I, H), "expert_down": (H, I), "attn_q": (4096, H), "attn_kv": (512, H),
+              "attn_o": (H, 4096)}
+    per_token = {"expert_gate_up": 48 * 2 * K, "expert_down": 48 * K, "attn_q": 48, "attn_kv": 48 * 2, "attn_o": 48}
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    res = {}
+    for n, (O, Ii) in shapes.items():
+        mats = []
+        for k in range(8):  # 8 distinct keyed matrices per shape
+            w, s = synth.block_quantize(rng.normal(0.0, 0.02, size=(O, Ii)).astype(np.float32))
+            mats.append((w, s, moe.Fp8Matrix.expert_key(7, 100 + 8 * list(shapes).index(n) + k, 0)))
+        x = rng.normal(size=(1, Ii)).astype(np.float32)
+        y = np.zeros((1, O), np.float32)
+        for w, s, key in mats:  # uploads (misses)
+            assert hip.colizig_cuda_matmul_fp8(p(y), p(x), p(w), p(s), 1, Ii, O, key) == 0
+        reps = max(1, args.steps // 4)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for w, s, key in mats:
+                hip.colizig_cuda_matmul_fp8(p(y), p(x), p(w), p(s), 1, Ii, O, key)
+        us = (time.perf_counter() - t0) * 1e6 / (reps * len(mats))
+        ref = oracle_matmul(x, mats[-1][0], mats[-1][1], 1, Ii, O)
+        err = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+        res[n] = {"us_per_call": round(us, 2), "calls_per_token": per_token[n], "rel_l2_vs_oracle": err}
+        log(f"dropin {n} {O}x{Ii}: {us:.2f} us per call (rel L2 {err:.1e})")
+    tok_ms = sum(v["us_per_call"] * v["calls_per_token"] for v in res.values()) / 1000.0
+    hits = ctypes.c_uint64()
+    misses = ctypes.c_uint64()
+    hip.colizig_cuda_stats(ctypes.byref(hits), ctypes.byref(misses), None, None)
+    line = {
+        "metric": "drop-in per-matmul calls (colizig_cuda_matmul_fp8, keyed hits, host buffers), Qwen3-30B-A3B "
+                  "expert and attention shapes, 1 MI355X",
+        "value": round(1000.0 / tok_ms, 2), "unit": "tok/s (FP8 matmul calls only)", "n_gpus": 1,
+        "steps": args.steps, "warmup": 0, "ms_per_step": round(tok_ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "e4m3-weights/f32-accumulate",
+        "data": "synthetic (N(0,0.02) block-FP8 weights, N(0,1) inputs)",
+        "config": {"workload": "dropin-per-matmul", "layers": 48, "hidden": H, "inter": I, "topk": K,
+                   "calls_per_token": sum(per_token.values())},
+        "calls": res, "cache_hits": hits.value, "cache_misses": misses.value,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def oracle_matmul(x, w, s, S, I, O):
+    from oracle import oracle as orc
+    return orc.matmul_fp8(x, w, s, S, I, O)
 
 
 def calibrate_copy(mib: int) -> None:

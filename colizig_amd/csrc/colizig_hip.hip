@@ -1143,6 +1143,9 @@ static int cache_slot_for(uint64_t key, size_t wb, size_t sb) {
     return victim;
 }
 
+void launch_matmul_fp8(float *y, const float *x, const uint8_t *w, const float *s, int S, int I, int O,
+                       hipStream_t st);
+
 extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, const float *scales, int S,
                                        int I, int O, uint64_t key) {
     CsrGuard csr;
@@ -1197,8 +1200,8 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
         wdev = g.d_w;
         sdev = g.d_s;
     }
-    k_gemm_fp8_generic<<<(O + 3) / 4, 256, 0, g.stream>>>((float *)g.d_y, (const float *)g.d_x,
-                                                          (const uint8_t *)wdev, (const float *)sdev, S, I, O);
+    launch_matmul_fp8((float *)g.d_y, (const float *)g.d_x, (const uint8_t *)wdev, (const float *)sdev, S, I, O,
+                      g.stream);
     if (hipGetLastError() != hipSuccess) return -4;
     if (hipMemcpyAsync(g.h_stage, g.d_y, yb, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return -5;
     if (hipStreamSynchronize(g.stream) != hipSuccess) return -5;
@@ -1213,14 +1216,28 @@ extern "C" int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned 
 constexpr int kGemvRows2Blocks = 256;
 
 template <int NB>
-void launch_gemv_fp8(float *y, const float *x, const Slot &sl, int S, int O, hipStream_t st) {
+void launch_gemv_fp8(float *y, const float *x, const uint8_t *w, const float *s, int S, int O, hipStream_t st) {
     constexpr int ST = NB >= 32 ? 128 / NB : 4;  // tokens staged per pass: at most 32 KiB of LDS
-    const uint8_t *w = (const uint8_t *)sl.w;
-    const float *s = (const float *)sl.s;
     if ((O + 7) / 8 >= kGemvRows2Blocks)
         k_gemv_fp8<NB, ST, 2><<<(O + 7) / 8, 256, 0, st>>>(y, x, w, s, (uint32_t)S, (uint32_t)O);
     else
         k_gemv_fp8<NB, ST, 1><<<(O + 3) / 4, 256, 0, st>>>(y, x, w, s, (uint32_t)S, (uint32_t)O);
+}
+
+// y[S][O] = x[S][I] . dequant(W)^T on device pointers (matmulFp8's
+// contract, fp8.zig:215-257): the row-parallel GEMV for I = 64 x {4, 8, 16,
+// 32, 48, 64} (rows 16-byte aligned), else the generic kernel.
+void launch_matmul_fp8(float *y, const float *x, const uint8_t *w, const float *s, int S, int I, int O,
+                       hipStream_t st) {
+    switch ((I % 64) ? 0 : I / 64) {
+        case 4: launch_gemv_fp8<4>(y, x, w, s, S, O, st); return;
+        case 8: launch_gemv_fp8<8>(y, x, w, s, S, O, st); return;
+        case 16: launch_gemv_fp8<16>(y, x, w, s, S, O, st); return;
+        case 32: launch_gemv_fp8<32>(y, x, w, s, S, O, st); return;
+        case 48: launch_gemv_fp8<48>(y, x, w, s, S, O, st); return;
+        case 64: launch_gemv_fp8<64>(y, x, w, s, S, O, st); return;
+        default: k_gemm_fp8_generic<<<(O + 3) / 4, 256, 0, st>>>(y, x, w, s, S, I, O); return;
+    }
 }
 
 extern "C" int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O) {
@@ -1335,18 +1352,7 @@ extern "C" int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int 
     sl.clock = ++g.lru;
     g.hits++;
     const hipStream_t st = pick_stream(stream);
-    switch ((I % 64) ? 0 : I / 64) {
-        case 4: launch_gemv_fp8<4>(y_dev, x_dev, sl, S, O, st); break;
-        case 8: launch_gemv_fp8<8>(y_dev, x_dev, sl, S, O, st); break;
-        case 16: launch_gemv_fp8<16>(y_dev, x_dev, sl, S, O, st); break;
-        case 32: launch_gemv_fp8<32>(y_dev, x_dev, sl, S, O, st); break;
-        case 48: launch_gemv_fp8<48>(y_dev, x_dev, sl, S, O, st); break;
-        case 64: launch_gemv_fp8<64>(y_dev, x_dev, sl, S, O, st); break;
-        default:
-            k_gemm_fp8_generic<<<(O + 3) / 4, 256, 0, st>>>(y_dev, x_dev, (const uint8_t *)sl.w, (const float *)sl.s,
-                                                           S, I, O);
-            break;
-    }
+    launch_matmul_fp8(y_dev, x_dev, (const uint8_t *)sl.w, (const float *)sl.s, S, I, O, st);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_err, sizeof g_err, "matmul_fp8_dev launch: %s", hipGetErrorString(e));
