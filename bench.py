@@ -98,6 +98,9 @@ def main():
     ap.add_argument("--split-slabs", action="store_true",
                     help="stream: weights and scales in two host slabs (two copies per fill) instead of one packed slab")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
+    ap.add_argument("--prefill-mfma", choices=["f16", "fp8"], default=None,
+                    help="prefill/qwen4: the grouped GEMMs on f16 MFMA (weights widened, activations f16 hi + lo) "
+                         "or FP8 MFMA (E4M3 weights, activations as three E4M3 terms); default: the library's")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -252,6 +255,12 @@ def prefill_bench(args) -> None:
     name = moe.init()
     log(f"device: {name}")
     hip = _lib.hip()
+    if args.prefill_mfma:
+        hip.colizig_hip_set_prefill_fp8(1 if args.prefill_mfma == "fp8" else 0)
+    fp8 = hip.colizig_hip_set_prefill_fp8(0) == 1
+    hip.colizig_hip_set_prefill_fp8(1 if fp8 else 0)
+    c["mfma"] = "fp8 (v_mfma_scale_f32_32x32x64_f8f6f4, activations as 3 E4M3 terms)" if fp8 else \
+        "f16 (v_mfma_f32_32x32x16_f16, activations as f16 hi + lo)"
     d = moe.dims(H, E, K, I, 0, True)
     zero_router = np.zeros((E, H), np.float32)
     for l in range(NL):
@@ -295,13 +304,17 @@ def prefill_bench(args) -> None:
         "metric": "MoE prefill tok/s (512-token step, Zipf(1.1) routing), Qwen3-30B-A3B shape, 1 MI355X",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "e4m3-weights/f16x2-activations/f32-accumulate",
+        "dtype": "e4m3-weights/e4m3x3-activations/f32-accumulate" if fp8 else "e4m3-weights/f16x2-activations/f32-accumulate",
         "data": "synthetic (seeded N(0,0.02) weights generated in HBM, N(0,1) hidden states)",
         "config": {**c, "parallelism": "none (1 GPU)", "global_batch": S, "seq_len": S},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole step",
                      "bytes_per_step": step_bytes},
         "mfma_tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
+        # useful FLOPs / step time against the dense peak of the MFMA in use
+        # (FP8 5.0 PFLOP/s, f16 2.5 PFLOP/s; the activation terms multiply the work done)
+        "mfma_peak_tflops": 5000.0 if fp8 else 2500.0,
+        "mfma_frac": round(step_flops / (ms * 1e-3) / 1e12 / (5000.0 if fp8 else 2500.0), 4),
         "experts_touched_per_layer": [min(touched), max(touched)],
     }
     print(json.dumps(line), flush=True)

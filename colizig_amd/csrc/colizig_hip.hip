@@ -132,6 +132,8 @@ struct Work {
     uint32_t *counts = nullptr, *offsets = nullptr, *sorted_slot = nullptr, *slot_pos = nullptr,
              *tok_order = nullptr, *tile_expert = nullptr, *tile_row0 = nullptr, *ntiles = nullptr;
     float *o = nullptr, *os = nullptr;
+    uint8_t *xq = nullptr, *xe = nullptr, *hq = nullptr, *he = nullptr, *hsq = nullptr, *hse = nullptr;
+    size_t cap_xq = 0, cap_xe = 0, cap_hq = 0, cap_he = 0, cap_hsq = 0, cap_hse = 0;
     _Float16 *xh = nullptr, *xl = nullptr, *hh = nullptr, *hl = nullptr, *hsh = nullptr, *hsl = nullptr;
     size_t cap_counts = 0, cap_offsets = 0, cap_sorted = 0, cap_slot_pos = 0, cap_tok_order = 0, cap_tiles = 0,
            cap_tiles2 = 0, cap_ntiles = 0, cap_o = 0, cap_os = 0, cap_xh = 0, cap_xl = 0, cap_hh = 0, cap_hl = 0,
@@ -242,6 +244,7 @@ struct Ctx {
     int64_t next_handle = 1;
     StreamPool pool;
     FusedState fused;
+    bool prefill_fp8 = false;  // grouped GEMMs on FP8 MFMA (k_gg8) instead of f16 (k_gg)
 };
 
 Ctx g;
@@ -337,7 +340,12 @@ int ensure_work_grouped(const colizig_dims &d, int S) {
         grow(&w.xh, &w.cap_xh, s * d.hidden) || grow(&w.xl, &w.cap_xl, s * d.hidden) ||
         grow(&w.hh, &w.cap_hh, sk * d.inter) || grow(&w.hl, &w.cap_hl, sk * d.inter) ||
         grow(&w.hsh, &w.cap_hsh, std::max<size_t>(1, s * d.shared_inter)) ||
-        grow(&w.hsl, &w.cap_hsl, std::max<size_t>(1, s * d.shared_inter))) {
+        grow(&w.hsl, &w.cap_hsl, std::max<size_t>(1, s * d.shared_inter)) ||
+        (g.prefill_fp8 &&
+         (grow(&w.xq, &w.cap_xq, 3 * s * d.hidden) || grow(&w.xe, &w.cap_xe, 3 * s * d.hidden / 32) ||
+          grow(&w.hq, &w.cap_hq, 3 * sk * d.inter) || grow(&w.he, &w.cap_he, 3 * sk * d.inter / 32) ||
+          grow(&w.hsq, &w.cap_hsq, std::max<size_t>(1, 3 * s * d.shared_inter)) ||
+          grow(&w.hse, &w.cap_hse, std::max<size_t>(1, 3 * s * d.shared_inter / 32))))) {
         snprintf(g_err, sizeof g_err, "grouped scratch allocation failed (S=%d)", S);
         return -2;
     }
@@ -679,7 +687,8 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
     const LayerDev &L = A.L;
     Work &w = g.work;
-    if (rms) {  // the RMS rows kernel writes the f16 split of xn for the gate/up GEMMs
+    const bool f8 = g.prefill_fp8;
+    if (rms && !f8) {  // the RMS rows kernel writes the f16 split of xn for the gate/up GEMMs
         A.xh = w.xh;
         A.xl = w.xl;
     }
@@ -708,8 +717,8 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.tile_row0 = w.tile_row0;
     G.ntiles = w.ntiles;
     G.max_tiles = grouped_max_tiles(Lh.d, S);
-    G.xh = rms ? nullptr : w.xh;  // no RMS rows kernel: the routing kernel splits x
-    G.xl = rms ? nullptr : w.xl;
+    G.xh = rms || f8 ? nullptr : w.xh;  // no RMS rows kernel: the routing kernel splits x
+    G.xl = rms || f8 ? nullptr : w.xl;
     G.hh = w.hh;
     G.hl = w.hl;
     G.hsh = w.hsh;
@@ -727,6 +736,12 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     }
     k_dispatch<<<1, 1024, 0, st>>>(G);
     const uint32_t mts = (uint32_t)(S + CZ_GG_M - 1) / CZ_GG_M;
+    const uint64_t sk = (uint64_t)S * L.K;
+    auto quant3 = [&](const float *src, uint64_t rows, uint32_t K, uint8_t *q, uint8_t *e) {
+        const uint64_t n = rows * (K / 32);
+        k_quant3<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(src, (uint32_t)rows, K, q, rows * K, e, rows * K / 32);
+    };
+    if (f8) quant3(G.xn, (uint64_t)S, L.H, w.xq, w.xe);
     // gate/up
     GGProblem P{};
     P.w0 = L.ew;
@@ -743,6 +758,13 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     P.c_hi = w.hh;
     P.c_lo = w.hl;
     P.routed = 1;
+    if (f8) {
+        P.aq = w.xq;
+        P.ae = w.xe;
+        P.aq_plane = (uint64_t)S * L.H;
+        P.ae_plane = (uint64_t)S * L.H / 32;
+        P.c = w.h;
+    }
     constexpr uint32_t cu = cz_gg_cols<GG_GATEUP>(), cd = cz_gg_cols<GG_DOWN>();
     // the shared expert's items run in the same launches as the routed ones
     GGProblem Q{};
@@ -757,11 +779,19 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.N = L.SI;
         Q.c_hi = w.hsh;
         Q.c_lo = w.hsl;
+        Q.c = w.hs;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
     }
     const uint32_t qu = L.SI ? (mts * (L.SI / cu) + 7) / 8 * 8 : 0u;
-    k_gg<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
+    if (f8)
+        k_gg8<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
+    else
+        k_gg<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
+    if (f8) {
+        quant3(w.h, sk, L.I, w.hq, w.he);
+        if (L.SI) quant3(w.hs, (uint64_t)S, L.SI, w.hsq, w.hse);
+    }
     // down
     GGProblem D{};
     D.w0 = L.ew + 2ull * L.I * L.H;
@@ -775,6 +805,10 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     D.a_lo = w.hl;
     D.c = w.o;
     D.routed = 1;
+    D.aq = w.hq;
+    D.ae = w.he;
+    D.aq_plane = sk * L.I;
+    D.ae_plane = sk * L.I / 32;
     GGProblem QD{};
     if (L.SI) {
         QD = D;
@@ -789,9 +823,16 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         QD.c = w.os;
         QD.routed = 0;
         QD.rows_total = (uint32_t)S;
+        QD.aq = w.hsq;
+        QD.ae = w.hse;
+        QD.aq_plane = (uint64_t)S * L.SI;
+        QD.ae_plane = (uint64_t)S * L.SI / 32;
     }
     const uint32_t qd = L.SI ? (mts * (L.H / cd) + 7) / 8 * 8 : 0u;
-    k_gg<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
+    if (f8)
+        k_gg8<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
+    else
+        k_gg<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
     k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
     if (Lh.shn_dtype >= 0) {
         if (int rc = launch_shared_native_add(Lh, out, S, st)) return rc;
@@ -1077,7 +1118,8 @@ extern "C" void colizig_cuda_shutdown(void) {
                     (void *)w.sorted_slot, (void *)w.slot_pos, (void *)w.tok_order, (void *)w.tile_expert,
                     (void *)w.tile_row0, (void *)w.ntiles, (void *)w.o, (void *)w.os, (void *)w.xh, (void *)w.xl,
                     (void *)w.hh, (void *)w.hl, (void *)w.hsh, (void *)w.hsl, (void *)w.ng, (void *)w.nu,
-                    (void *)w.no, (void *)w.nsg})
+                    (void *)w.no, (void *)w.nsg, (void *)w.xq, (void *)w.xe, (void *)w.hq, (void *)w.he,
+                    (void *)w.hsq, (void *)w.hse})
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     for (void *p : {(void *)g.fused.r, (void *)g.fused.p, (void *)g.fused.zero, (void *)g.fused.lgx,
@@ -3209,6 +3251,16 @@ extern "C" int colizig_hip_memset(void *dst, int value, uint64_t bytes) {
     return 0;
 }
 extern "C" void *colizig_hip_stream(void) { return g.inited ? (void *)g.stream : nullptr; }
+
+// The prefill's grouped GEMMs on FP8 MFMA (1) or f16 MFMA (0); returns the
+// previous setting.
+extern "C" int colizig_hip_set_prefill_fp8(int enable) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = g.prefill_fp8 ? 1 : 0;
+    g.prefill_fp8 = enable != 0;
+    return prev;
+}
 
 extern "C" int colizig_hip_set_fused_decode(int enable) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);

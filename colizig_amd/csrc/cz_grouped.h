@@ -325,6 +325,11 @@ struct GGProblem {
     float *c;               // DOWN: O rows [rows][N]
     int routed;             // 1: tiles from the dispatch table; 0: shared (rows = tokens in order)
     uint32_t rows_total;    // shared: S
+    // FP8-MFMA form (k_gg8): A rows as three E4M3 terms with E8M0 exponents
+    // per 32 columns (cz_quant3); GATEUP writes h as f32 rows to c
+    const uint8_t *aq;      // [3][rows][Kd] (term planes aq_plane bytes apart)
+    const uint8_t *ae;      // [3][rows][Kd/32] (planes ae_plane bytes apart)
+    uint64_t aq_plane, ae_plane;
 };
 
 // Output columns of one workgroup: 4 waves x 2 subtiles of 32 columns.  A
@@ -598,6 +603,273 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem PR, GGProb
             const uint64_t o = (uint64_t)dst * P.N + ncol[0];
             P.c_hi[o] = hi;
             P.c_lo[o] = (_Float16)(v - (float)hi);
+        } else {
+#pragma unroll
+            for (int m = 0; m < 2; ++m) P.c[(uint64_t)dst * P.N + ncol[m]] = acc[m][i] * cur[m];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// FP8-MFMA grouped GEMM (the prefill's alternative to k_gg): the E4M3 weights
+// go straight into v_mfma_scale_f32_32x32x64_f8f6f4 as the B operand; the A
+// rows (x for gate/up, h for down) come as three E4M3 terms, each with an
+// E8M0 exponent per 32 columns (x ~= sum_t 2^(e_t - 127) q_t, about 12
+// significant bits), applied by the instruction itself.  Lane layout of one
+// 32 x 32 x 64 product (checked on the device): lane l gives row (or
+// column) l % 32; its bytes 0-15 are K positions 16 (l/32) + 0..15 of the
+// first 32-column group, bytes 16-31 positions 32 + 16 (l/32) + 0..15 of the
+// second; the exponent of row m, group b comes from lane m + 32 b.
+// ---------------------------------------------------------------------------
+
+// E4M3 of v (|v| <= 448), round to nearest even; byte in the low 8 bits.
+__device__ __forceinline__ uint32_t cz_f32_to_e4m3(float v) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xffu;
+}
+
+// Rows of K columns (K % 32 == 0) to three E4M3 terms: one thread per 32
+// columns of a row.  Term t: k_t = the least k with max|r_t| <= 448 * 2^k
+// over the group (r_0 = x), q_t = e4m3(r_t * 2^-k_t), r_{t+1} = r_t -
+// 2^k_t * q_t (exact: q_t rounds r_t * 2^-k_t); exponent byte k_t + 127, or
+// 0 with q_t = 0 for an all-zero group.
+__global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, uint32_t rows, uint32_t K,
+                                               uint8_t *__restrict__ q, uint64_t q_plane, uint8_t *__restrict__ e,
+                                               uint64_t e_plane) {
+    const uint32_t ng = K / 32;
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (uint64_t)rows * ng) return;
+    const uint64_t row = gid / ng, grp = gid - row * ng;
+    const float4 *p = reinterpret_cast<const float4 *>(src + row * K + grp * 32);
+    float r[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 v = p[i];
+        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, __builtin_fabsf(r[i]));
+        int k = 0;
+        uint32_t eb = 0;
+        if (amax > 0.0f) {
+            const int ef = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xffu);
+            k = (ef ? ef - 127 : -127) - 8;  // floor(log2 amax) - 8 (subnormals: below -127)
+            if (amax > __builtin_ldexpf(448.0f, k)) ++k;
+            k = max(-126, min(k, 127));
+            eb = (uint32_t)(k + 127);
+        }
+        const float inv = amax > 0.0f ? __builtin_ldexpf(1.0f, -k) : 0.0f;
+        const float sc = amax > 0.0f ? __builtin_ldexpf(1.0f, k) : 0.0f;
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t b = amax > 0.0f ? cz_f32_to_e4m3(r[4 * i + j] * inv) : 0u;
+                word |= b << (8 * j);
+            }
+            w[i] = word;
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const cz_float2 d = j ? cz_fp8x2_hi(word) : cz_fp8x2_lo(word);
+                r[4 * i + j] = r[4 * i + j] - d.x * sc;
+                r[4 * i + j + 1] = r[4 * i + j + 1] - d.y * sc;
+            }
+        }
+        uint4 *qo = reinterpret_cast<uint4 *>(q + t * q_plane + row * K + grp * 32);
+        qo[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        qo[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        e[t * e_plane + row * ng + grp] = (uint8_t)eb;
+    }
+}
+
+typedef int cz_i8x32 __attribute__((ext_vector_type(8)));
+
+// A tile of one K block in LDS for k_gg8: 3 term planes x CZ_GG_M rows x 128
+// bytes (8 chunks of 16 B; chunk c of row r at c ^ (r & 7)), then the
+// exponents: 3 planes x CZ_GG_M rows x 4 bytes.
+#define CZ_GG8_APLANE (CZ_GG_M * 128)
+#define CZ_GG8_EOFF (3 * CZ_GG8_APLANE)
+__device__ __forceinline__ uint32_t cz_gg8_off(uint32_t r, uint32_t c) { return r * 128u + ((c ^ (r & 7u)) << 4); }
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGProblem PS) {
+    constexpr uint32_t NCOL = cz_gg_cols<MODE>();
+    const uint32_t ns = PS.N ? (PS.rows_total + CZ_GG_M - 1) / CZ_GG_M * (PS.N / NCOL) : 0u;
+    const uint32_t ns8 = (ns + 7u) & ~7u;
+    const bool sh = blockIdx.x < ns8;
+    if (sh && blockIdx.x >= ns) return;  // block-uniform
+    const GGProblem P = sh ? PS : PR;
+    __shared__ __align__(16) uint8_t lds0[CZ_GG8_EOFF + 3 * CZ_GG_M * 4];
+    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_WLD];
+    __shared__ uint32_t s_rowsrc[CZ_GG_M];
+    __shared__ uint32_t s_rowdst[CZ_GG_M];
+
+    const uint32_t lane = cz_lane(), tid = threadIdx.x;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t ntn = P.N / NCOL;
+    uint32_t t = blockIdx.x;
+    if (!sh) {
+        const uint32_t b = blockIdx.x - ns8;
+        const uint32_t mtiles = P.routed ? G.ntiles[0] : (P.rows_total + CZ_GG_M - 1) / CZ_GG_M;
+        const uint32_t T = mtiles * ntn, per = (T + 7) / 8;
+        const uint32_t j = b >> 3;
+        t = (b & 7) * per + j;
+        if (j >= per || t >= T) return;  // block-uniform
+    }
+    const uint32_t mt = t / ntn, nt = t - mt * ntn;
+    uint32_t e = 0, row0, rows;
+    if (P.routed) {
+        e = G.tile_expert[mt];
+        row0 = G.tile_row0[mt];
+        rows = min((uint32_t)CZ_GG_M, G.offsets[e + 1] - row0);
+    } else {
+        row0 = mt * CZ_GG_M;
+        rows = min((uint32_t)CZ_GG_M, P.rows_total - row0);
+    }
+    if (tid < CZ_GG_M) {
+        const uint32_t pos = row0 + min(tid, rows - 1);
+        s_rowsrc[tid] = (MODE == GG_GATEUP && P.routed) ? G.sorted_slot[pos] / G.L.K : pos;
+        s_rowdst[tid] = tid < rows ? row0 + tid : ~0u;
+    }
+    __syncthreads();
+    // A staging: thread t moves chunk t%8 of row t/8 of each term plane;
+    // threads < 96 move one 4-byte exponent word (plane t/32, row t%32)
+    const uint32_t ar = tid >> 3, ac = tid & 7u;
+    const uint64_t a_src = (uint64_t)s_rowsrc[ar] * P.Kd + ac * 16u;
+    const uint32_t a_dst = cz_gg8_off(ar, ac);
+    const uint32_t nbe = P.Kd / 32u;
+    const uint32_t ep = tid >> 5, er = tid & 31u;
+    const uint64_t e_src = ep * P.ae_plane + (uint64_t)s_rowsrc[min(er, (uint32_t)CZ_GG_M - 1)] * nbe;
+
+    const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
+    const uint8_t *W0 = P.w0 + sl * P.w_stride;
+    const float *S0 = P.s0 + sl * P.s_stride;
+    const uint8_t *wbase[2];
+    const float *srow[2];
+    uint32_t ncol[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const uint32_t nb = MODE == GG_GATEUP ? nt * NCOL + wave * 32u : nt * NCOL + wave * 64u + 32u * m;
+        ncol[m] = nb + (lane & 31u);
+        const uint64_t moff = (MODE == GG_GATEUP && m) ? P.w1_off : 0;
+        const uint64_t soff = (MODE == GG_GATEUP && m) ? P.s1_off : 0;
+        wbase[m] = W0 + moff + (uint64_t)nb * P.Kd;
+        srow[m] = S0 + soff + (uint64_t)(nb / CZ_BLOCK) * P.nbK;
+    }
+    uint8_t *lw = ldsw[wave];
+    const uint32_t wl_off = (lane >> 3) * P.Kd + (lane & 7u) * 16u;
+    const uint32_t wl_lds = (lane >> 3) * CZ_GG_WLD + (lane & 7u) * 16u;
+
+    cz_float16v acc[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
+    float cur[2] = {0.0f, 0.0f};
+    const uint32_t nkb = P.Kd / CZ_GG_KB;
+    const uint8_t *gl0 = wbase[0] + wl_off, *gl1 = wbase[1] + wl_off;
+    const uint64_t r8 = 8ull * P.Kd;
+    uint4 x0, x1, x2, x3, x4, x5, x6, x7, q0, q1, q2;
+    uint32_t ev = 0;
+#define CZ_GG8_LOAD(kb_)                                                        \
+    {                                                                           \
+        const uint64_t ko_ = (uint64_t)(kb_) * CZ_GG_KB;                        \
+        q0 = *(const uint4 *)(P.aq + a_src + ko_);                              \
+        q1 = *(const uint4 *)(P.aq + P.aq_plane + a_src + ko_);                 \
+        q2 = *(const uint4 *)(P.aq + 2 * P.aq_plane + a_src + ko_);             \
+        if (tid < 96) ev = *(const uint32_t *)(P.ae + e_src + (kb_) * 4u);      \
+        x0 = *(const uint4 *)(gl0 + ko_);                                       \
+        x1 = *(const uint4 *)(gl0 + r8 + ko_);                                  \
+        x2 = *(const uint4 *)(gl0 + 2 * r8 + ko_);                              \
+        x3 = *(const uint4 *)(gl0 + 3 * r8 + ko_);                              \
+        x4 = *(const uint4 *)(gl1 + ko_);                                       \
+        x5 = *(const uint4 *)(gl1 + r8 + ko_);                                  \
+        x6 = *(const uint4 *)(gl1 + 2 * r8 + ko_);                              \
+        x7 = *(const uint4 *)(gl1 + 3 * r8 + ko_);                              \
+    }
+#define CZ_GG8_STORE()                                                          \
+    {                                                                           \
+        *(uint4 *)(lds0 + a_dst) = q0;                                          \
+        *(uint4 *)(lds0 + CZ_GG8_APLANE + a_dst) = q1;                          \
+        *(uint4 *)(lds0 + 2 * CZ_GG8_APLANE + a_dst) = q2;                      \
+        if (tid < 96) *(uint32_t *)(lds0 + CZ_GG8_EOFF + 4u * tid) = ev;        \
+        uint8_t *d_ = lw + wl_lds;                                              \
+        *(uint4 *)(d_) = x0;                                                    \
+        *(uint4 *)(d_ + 1 * 8 * CZ_GG_WLD) = x1;                                 \
+        *(uint4 *)(d_ + 2 * 8 * CZ_GG_WLD) = x2;                                 \
+        *(uint4 *)(d_ + 3 * 8 * CZ_GG_WLD) = x3;                                 \
+        *(uint4 *)(d_ + 4 * 8 * CZ_GG_WLD) = x4;                                 \
+        *(uint4 *)(d_ + 5 * 8 * CZ_GG_WLD) = x5;                                 \
+        *(uint4 *)(d_ + 6 * 8 * CZ_GG_WLD) = x6;                                 \
+        *(uint4 *)(d_ + 7 * 8 * CZ_GG_WLD) = x7;                                 \
+    }
+    CZ_GG8_LOAD(0)
+    CZ_GG8_STORE()
+    CZ_GG8_LOAD(min(1u, nkb - 1))
+    __syncthreads();
+    const uint32_t rl = lane & 31u, hh = lane >> 5;
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        // block scales folded into acc as in k_gg (cz_gg_rescale): acc is
+        // rescaled by cur / s, and a zero-scale block's weights are masked
+        // to +0 as they are read
+        uint32_t keep[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const float sc = cz_const_f32(srow[m] + kb);
+            const bool zero = sc == 0.0f;
+            const float rr = (zero || cur[m] == 0.0f) ? 1.0f : cur[m] / sc;
+            cur[m] = zero ? cur[m] : sc;
+            keep[m] = zero ? 0u : ~0u;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[m][i] *= rr;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            // the wave's weights in MFMA layout: subtile m, K half kk: row 32m
+            // + lane%32, bytes 64kk + 16(l/32) and 64kk + 32 + 16(l/32)
+            cz_i8x32 bm[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const uint8_t *rowp = lw + (32u * m + rl) * CZ_GG_WLD + 64u * kk + 16u * hh;
+                const uint4 lo = *(const uint4 *)rowp, hi = *(const uint4 *)(rowp + 32u);
+                const uint32_t k_ = keep[m];
+                bm[m] = cz_i8x32{(int)(lo.x & k_), (int)(lo.y & k_), (int)(lo.z & k_), (int)(lo.w & k_),
+                                 (int)(hi.x & k_), (int)(hi.y & k_), (int)(hi.z & k_), (int)(hi.w & k_)};
+            }
+#pragma unroll
+            for (int tt = 0; tt < 3; ++tt) {
+                const uint8_t *pl = lds0 + tt * CZ_GG8_APLANE;
+                const uint4 lo = *(const uint4 *)(pl + cz_gg8_off(rl, 4u * kk + hh));
+                const uint4 hi = *(const uint4 *)(pl + cz_gg8_off(rl, 4u * kk + 2u + hh));
+                const cz_i8x32 am = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z,
+                                     (int)hi.w};
+                // exponent of row lane%32, group 2 kk + lane/32 of this K block
+                const int sa = (int)lds0[CZ_GG8_EOFF + (tt * CZ_GG_M + rl) * 4u + 2u * kk + hh];
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    acc[m] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(am, bm[m], acc[m], 0, 0, 0, sa, 0, 127);
+            }
+        }
+        if (kb + 1 < nkb) {  // block-uniform
+            __syncthreads();
+            CZ_GG8_STORE()
+            CZ_GG8_LOAD(min(kb + 2, nkb - 1))
+            __syncthreads();
+        }
+    }
+#undef CZ_GG8_LOAD
+#undef CZ_GG8_STORE
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
+        const uint32_t dst = s_rowdst[r];
+        if (dst == ~0u) continue;
+        if constexpr (MODE == GG_GATEUP) {
+            P.c[(uint64_t)dst * P.N + ncol[0]] = cz_silu_fast(acc[0][i] * cur[0]) * (acc[1][i] * cur[1]);
         } else {
 #pragma unroll
             for (int m = 0; m < 2; ++m) P.c[(uint64_t)dst * P.N + ncol[m]] = acc[m][i] * cur[m];
