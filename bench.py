@@ -76,7 +76,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--parity-layers", type=int, default=4)
+    ap.add_argument("--parity-layers", type=int, default=48,
+                    help="decode: layers of the parity check against the oracle's own chain (one token)")
     ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead", "dropin"],
                     default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
@@ -195,15 +196,23 @@ def main():
     log(f"kernels: layer {layer_us:.2f} us ({layer_gbs:.0f} GB/s of {layer_bytes} algorithmic bytes), "
         f"final residual {final_us:.2f} us")
 
+    # host copies of the layers for the oracle (parity and CPU baseline)
+    hosts, copy_s = None, 0.0
+    if args.parity_layers > 0 or not args.no_cpu:
+        from oracle import oracle as orc
+        t1 = time.time()
+        n_host = NL if not args.no_cpu else min(args.parity_layers, NL)
+        hosts = [orc.OracleLayer(host_layer(hip, L, c)) for L in layers[:n_host]]
+        copy_s = time.time() - t1
     # parity: the oracle's own chain from the same x0 over the first layers
     parity = None
     if args.parity_layers > 0:
-        parity = parity_check(hip, moe, layers[:args.parity_layers], x0, c, eps)
+        parity = parity_check(hip, moe, hosts[:min(args.parity_layers, NL)], x0, c, eps)
         log(f"parity: {parity}")
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(hip, moe, layers, x0, c, eps, args.cpu_seconds)
+        cpu = cpu_baseline(hosts, x0, eps, args.cpu_seconds, copy_s)
         log(f"cpu baseline: {cpu}")
 
     line = {
@@ -720,14 +729,13 @@ def calibrate_copy(mib: int) -> None:
     log(f"copied {mib} MiB x 3")
 
 
-def parity_check(hip, moe, layers, x0, c, eps):
+def parity_check(hip, moe, orcs, x0, c, eps):
     """The GPU chain and the oracle's own chain from the same x0 over the
-    given layers, one token: routing bit-exact (on the GPU's router input, and
-    the same picks as the oracle's chain), router input and residual stream
-    within 1e-3 relative L2."""
-    from oracle import oracle as orc
+    first len(orcs) layers, one token: routing bit-exact (on the GPU's router
+    input, and the same picks as the oracle's chain), router input and
+    residual stream within 1e-3 relative L2."""
     H, K = c["hidden"], c["topk"]
-    n = len(layers)
+    n = len(orcs)
     xn_t = moe.DeviceBuffer(n * H * 4)
     idx_t = moe.DeviceBuffer(n * K * 4)
     g_t = moe.DeviceBuffer(n * K * 4)
@@ -742,10 +750,17 @@ def parity_check(hip, moe, layers, x0, c, eps):
     xo = x0.copy()
     exact = True
     worst_xn = 0.0
-    for l, L in enumerate(layers):
-        O = orc.OracleLayer(host_layer(hip, L, c))
+    min_gap = 1 << 30
+    for l, O in enumerate(orcs):
         xn_o, idx_o, _ = O.chain(xo, eps)
         worst_xn = max(worst_xn, float(np.linalg.norm(xn[l] - xn_o[0]) / np.linalg.norm(xn_o[0])))
+        # near-tie census: the smallest gap, in f32 ulps, between consecutive
+        # post-exp values of the oracle's top K+1 (a gap of a few ulps would
+        # make the picks depend on the last bit of exp)
+        _, _, v = O.route(xn_o[0])
+        top = sorted(range(v.size), key=lambda e: (-float(v[e]), e))[:K + 1]
+        b = v[top].view(np.uint32).astype(np.int64)
+        min_gap = min(min_gap, int(np.min(b[:-1] - b[1:])))
         ri, rg, _ = O.route(xn[l])
         exact &= bool(np.array_equal(ri, idx[l]) and np.array_equal(rg.view(np.uint32), gates[l].view(np.uint32)))
         exact &= bool(np.array_equal(idx[l], idx_o[0]))
@@ -753,7 +768,8 @@ def parity_check(hip, moe, layers, x0, c, eps):
     for buf in (xn_t, idx_t, g_t, xtmp):
         buf.free()
     return {"layers_checked": n, "reference": "oracle chain from the same x0", "routing_bit_exact": exact,
-            "max_router_input_rel_l2": worst_xn, "residual_rel_l2": x_err, "tolerance": 1e-3}
+            "max_router_input_rel_l2": worst_xn, "residual_rel_l2": x_err, "tolerance": 1e-3,
+            "near_tie_min_gap_ulps": min_gap}
 
 
 def host_layer(hip, L, c):
@@ -777,12 +793,9 @@ def host_layer(hip, L, c):
                 router=L.read_router(), experts=experts, shared=None, _slabs=(ew, es))
 
 
-def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
+def cpu_baseline(hosts, x0, eps, seconds, copy_s):
     """The oracle's chain on the host cores, same weights, bounded sample."""
     from oracle import oracle as orc
-    t0 = time.time()
-    hosts = [orc.OracleLayer(host_layer(hip, L, c)) for L in layers]
-    copy_s = time.time() - t0
     # at most 16 host threads per GPU (the CPU share of a one-GPU host), whatever the affinity mask shows
     present = len(os.sched_getaffinity(0))
     threads = min(present, 16)
@@ -800,7 +813,7 @@ def cpu_baseline(hip, moe, layers, x0, c, eps, seconds):
     orc.lib().czo_parallel_disable()
     return {"value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "cores_present": present,
-            "sample": f"{n} decode tokens x {len(layers)} layers of the same workload (oracle chain, "
+            "sample": f"{n} decode tokens x {len(hosts)} layers of the same workload (oracle chain, "
                       f"expert fan-out over min(threads, top-k) tasks as parallel.chunks), {el:.1f}s",
             "cpu_model": cpu_model(), "host_copy_s": round(copy_s, 1)}
 
