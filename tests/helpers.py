@@ -56,10 +56,16 @@ def moe_f64(layer: dict, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
             cache[key] = deq_f64(ex[k + "_w"], ex[k + "_s"])
         return cache[key]
 
+    def native(m):  # NativeMatrix rows: f32, or BF16 bits (uint16) widened exactly
+        m = np.asarray(m)
+        if m.dtype == np.uint16:
+            return (m.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        return m.astype(np.float64)
+
     x = np.asarray(x, np.float64).reshape(-1, d["hidden"])
     out = np.zeros_like(x)
     idx = np.zeros((x.shape[0], K), np.int64)
-    R = np.asarray(layer["router"], np.float64)
+    R = native(layer["router"])
     for s in range(x.shape[0]):
         lg = R @ x[s]
         v = np.exp(lg - lg.max())
@@ -72,11 +78,16 @@ def moe_f64(layer: dict, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
             out[s] += (v[e] / den) * (mat(e, "down") @ h)
         if d["shared_inter"]:
             sh = layer["shared"]
-            g = deq_f64(sh["gate_w"], sh["gate_s"]) @ x[s]
-            u = deq_f64(sh["up_w"], sh["up_s"]) @ x[s]
+            if "native" in sh:
+                wg, wu, wd = native(sh["gate"]), native(sh["up"]), native(sh["down"])
+            else:
+                wg, wu = deq_f64(sh["gate_w"], sh["gate_s"]), deq_f64(sh["up_w"], sh["up_s"])
+                wd = deq_f64(sh["down_w"], sh["down_s"])
+            g = wg @ x[s]
+            u = wu @ x[s]
             h = g / (1 + np.exp(-g)) * u
             sg = 1 / (1 + np.exp(-(x[s] @ np.asarray(sh["sh_gate"], np.float64))))
-            out[s] += sg * (deq_f64(sh["down_w"], sh["down_s"]) @ h)
+            out[s] += sg * (wd @ h)
         idx[s] = order
     return out, idx
 

@@ -337,6 +337,30 @@ def test_moe_forward_vs_f64(oracle_lib, SI):
         assert rel_l2(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("shared", ["f32", "bf16"])
+def test_native_shared_and_bf16_router_vs_f64(oracle_lib, shared):
+    """NativeMatrix weights (tensors.zig:65-120): a BF16 router and an f32 or
+    BF16 shared expert evaluated as dense rows (moe.zig:467-479), against the
+    independent float64 MoE that widens BF16 bits itself.  Zeroing the shared
+    gate's weights moves the output (the shared term is present), and the
+    BF16 router's logits are the widened rows' dots (routing agrees)."""
+    from colizig_amd import synth
+    host = synth.with_native(_layer(SI=256, seed=41), seed=42, shared=shared)
+    assert host["router"].dtype == np.uint16
+    L = oracle_lib.OracleLayer(host)
+    x = np.random.default_rng(43).normal(size=(3, 512)).astype(np.float32)
+    for S in (1, 3):
+        out, idx, _ = L.forward(x[:S])
+        ref, ridx = moe_f64(host, x[:S])
+        assert np.array_equal(idx, ridx)
+        assert rel_l2(out, ref) < 1e-5
+    no_sh = dict(host, shared=dict(host["shared"], down=np.zeros_like(host["shared"]["down"])))
+    out0, _, _ = oracle_lib.OracleLayer(no_sh).forward(x)
+    ref0, _ = moe_f64(no_sh, x)
+    assert rel_l2(out0, ref0) < 1e-5
+    assert rel_l2(out0, out) > 1e-3
+
+
 def test_grouped_equals_dense_per_token(oracle_lib):
     """moe.zig:720-728: grouped prefill ~= per-token dense within 1e-3 abs,
     and (moe.zig:717-718) deterministic across fresh runs."""
