@@ -98,6 +98,9 @@ def main():
                          "the last token's routing")
     ap.add_argument("--split-slabs", action="store_true",
                     help="stream: weights and scales in two host slabs (two copies per fill) instead of one packed slab")
+    ap.add_argument("--fused-predict", type=int, default=None, choices=[0, 1],
+                    help="decode: request each layer's predicted experts before its routing (1, the library's "
+                         "default) or after it (0)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--prefill-mfma", choices=["f16", "fp8"], default=None,
                     help="prefill/qwen4: the grouped GEMMs on f16 MFMA (weights widened, activations f16 hi + lo) "
@@ -141,6 +144,11 @@ def main():
     name = moe.init()
     log(f"device: {name}")
     hip = _lib.hip()
+    if args.fused_predict is not None:
+        hip.colizig_hip_set_fused_predict(args.fused_predict)
+    predict = hip.colizig_hip_set_fused_predict(0)
+    hip.colizig_hip_set_fused_predict(predict)
+    c["expert_prediction"] = "next layer's top-k on this layer's router input" if predict else "off"
     d = moe.dims(H, E, K, I, 0, True)
     t0 = time.time()
     layers = []
@@ -166,6 +174,8 @@ def main():
 
     # timed region: K steps, synchronised on both sides
     ev0, ev1 = hip.colizig_hip_event_create(), hip.colizig_hip_event_create()
+    pst = np.zeros(2, np.uint64)
+    hip.colizig_hip_fused_predict_stats(pst.ctypes.data)  # zeroes the prediction counters
     assert hip.colizig_hip_sync() == 0
     w0 = time.perf_counter()
     hip.colizig_hip_event_record(ev0, None)
@@ -178,6 +188,10 @@ def main():
     ms_per_step = ms_total / args.steps
     tok_s = 1000.0 / ms_per_step
     log(f"timed: {args.steps} steps, {ms_per_step * 1000:.1f} us/token, {tok_s:.1f} tok/s (wall {wall:.3f}s)")
+    pred_rate = None
+    if hip.colizig_hip_fused_predict_stats(pst.ctypes.data) == 0 and pst[0] > 0:
+        pred_rate = round(float(pst[1]) / float(pst[0]), 4)
+        log(f"predicted experts picked: {int(pst[1])} of {int(pst[0])} ({pred_rate:.3f})")
 
     # the layer kernel's duration: a HIP graph of the layer launches replayed
     # between two events on the library stream (minus the chain's final
@@ -244,6 +258,7 @@ def main():
         },
         "kernels_us": {"layer": round(layer_us, 3), "final_residual": round(final_us, 3)},
         "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
+        "expert_prediction_hit_rate": pred_rate,
         "parity": parity,
         "cpu_baseline": cpu,
     }

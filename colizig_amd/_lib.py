@@ -94,6 +94,8 @@ SIGNATURES = {
                                                       ctypes.c_float, ctypes.c_int, vp]),
     "colizig_hip_expert_slab_read": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
     "colizig_hip_set_fused_decode": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_set_fused_predict": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_fused_predict_stats": (ctypes.c_int, [ctypes.c_void_p]),
     "colizig_hip_fused_decode_active": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]),
     "colizig_hip_chain_fused_times": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_float,
                                                      ctypes.c_int, vp]),

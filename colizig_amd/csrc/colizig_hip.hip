@@ -211,6 +211,10 @@ struct FusedState {
     float *zero = nullptr;           // [8][H] zeros: the first layer's partials
     unsigned long long *lgx = nullptr;  // [8][E] tagged logits
     unsigned long long *hx = nullptr;   // [K*I] tagged gated products
+    uint32_t *pred = nullptr;        // [2][64] predicted experts of the next layer, ping-pong
+    unsigned long long *lgpx = nullptr;  // [E] tagged next-layer logits
+    unsigned long long *pstat = nullptr;  // [2] slots predicted, predictions picked
+    int predict = 1;                 // colizig_hip_set_fused_predict
     uint32_t *run = nullptr;         // chain-run counter
     uint32_t *err_host = nullptr;    // host-coherent error word
     uint32_t *err_dev = nullptr;     // its device address
@@ -705,7 +709,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     G.gates = w.gates;
     G.sgate = w.sgate;
     G.sgate_ready = rms_rows_write_sgate(A) ? 1u : 0u;
-    G.usage = L.usage;
+    G.usage = nullptr;  // k_dispatch counts the round's picks per expert
     G.idx_trace = idx_trace;
     G.gates_trace = gates_trace;
     G.counts = w.counts;
@@ -734,6 +738,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         case 8: launch_route_tokens<8>(G, st); break;
         default: launch_route_tokens<16>(G, st); break;
     }
+    G.usage = L.usage;
     k_dispatch<<<1, 1024, 0, st>>>(G);
     const uint32_t mts = (uint32_t)(S + CZ_GG_M - 1) / CZ_GG_M;
     const uint64_t sk = (uint64_t)S * L.K;
@@ -849,19 +854,17 @@ LayerHost *find_layer(uint32_t layer);
 
 // The one-launch decode serves batch 1 on a device of 8 XCDs x 32 CUs for
 // resident layers without a shared expert with H in {512, 1024, 2048},
-// E <= 128, K*I a multiple of 1024 with K*I/1024 in {1, 2, 4, 6, 8} and I a
-// multiple of K*I/32 (each wave's down columns within one expert).
+// E <= 128, K <= 32, I a multiple of 128 and K*I/1024 in {1, 2, 4, 6, 8}.
 bool fused_ok(const LayerHost &L, int S) {
     const colizig_dims &d = L.d;
     if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG) return false;
-    if (d.shared_inter != 0 || d.experts > 128 || d.topk > CZ_MAX_K || d.inter % CZ_BLOCK || L.router_bf16)
+    if (d.shared_inter != 0 || d.experts > 128 || d.topk > 32 || d.inter % CZ_BLOCK || L.router_bf16)
         return false;
     if (d.hidden != 512 && d.hidden != 1024 && d.hidden != 2048) return false;
     const uint64_t ki = (uint64_t)d.topk * d.inter;
     if (ki % 1024) return false;
-    const uint64_t rw = ki / 1024, cw = ki / 32;
-    if (rw != 1 && rw != 2 && rw != 4 && rw != 6 && rw != 8) return false;
-    return d.inter % cw == 0;
+    const uint64_t rw = ki / 1024;
+    return rw == 1 || rw == 2 || rw == 4 || rw == 6 || rw == 8;
 }
 
 int ensure_fused(const colizig_dims &d) {
@@ -870,6 +873,9 @@ int ensure_fused(const colizig_dims &d) {
     if (!F.run) {
         if (hipMalloc(&F.run, 256) != hipSuccess) return -2;
         if (hipMemset(F.run, 0, 256) != hipSuccess) return -2;
+        F.pstat = reinterpret_cast<unsigned long long *>(F.run) + 16;  // bytes 128..143 of the same block
+        if (hipMalloc(&F.pred, 2 * 64 * sizeof(uint32_t)) != hipSuccess) return -2;
+        if (hipMemset(F.pred, 0, 2 * 64 * sizeof(uint32_t)) != hipSuccess) return -2;
         if (hipHostMalloc(&F.err_host, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) return -2;
         __atomic_store_n(F.err_host, 0u, __ATOMIC_RELEASE);
         if (hipHostGetDevicePointer((void **)&F.err_dev, F.err_host, 0) != hipSuccess) return -2;
@@ -886,11 +892,14 @@ int ensure_fused(const colizig_dims &d) {
         F.cap_h = d.hidden;
     }
     if (F.cap_e < d.experts) {
-        size_t cap = 0;
+        size_t cap = 0, cap_p = 0;
         if (F.lgx) g.retired.push_back(F.lgx);
+        if (F.lgpx) g.retired.push_back(F.lgpx);
         F.lgx = nullptr;
-        if (grow(&F.lgx, &cap, (size_t)CZ_NXCD * d.experts)) return -2;
+        F.lgpx = nullptr;
+        if (grow(&F.lgx, &cap, (size_t)CZ_NXCD * d.experts) || grow(&F.lgpx, &cap_p, (size_t)d.experts)) return -2;
         if (hipMemset(F.lgx, 0, cap * sizeof(unsigned long long)) != hipSuccess) return -2;
+        if (hipMemset(F.lgpx, 0, cap_p * sizeof(unsigned long long)) != hipSuccess) return -2;
         F.cap_e = d.experts;
     }
     if (F.cap_ki < ki) {
@@ -904,15 +913,23 @@ int ensure_fused(const colizig_dims &d) {
     return 0;
 }
 
+template <int NB, bool SPEC>
+void launch_fused_spec(const FusedArgs &A, uint32_t rw, hipStream_t st) {
+    switch (rw) {
+        case 1: k_layer_fused<NB, 1, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 2: k_layer_fused<NB, 2, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 4: k_layer_fused<NB, 4, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 6: k_layer_fused<NB, 6, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+        default: k_layer_fused<NB, 8, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+    }
+}
+
 template <int NB>
 void launch_fused_nb(const FusedArgs &A, uint32_t rw, hipStream_t st) {
-    switch (rw) {
-        case 1: k_layer_fused<NB, 1><<<CZ_FWG, 256, 0, st>>>(A); return;
-        case 2: k_layer_fused<NB, 2><<<CZ_FWG, 256, 0, st>>>(A); return;
-        case 4: k_layer_fused<NB, 4><<<CZ_FWG, 256, 0, st>>>(A); return;
-        case 6: k_layer_fused<NB, 6><<<CZ_FWG, 256, 0, st>>>(A); return;
-        default: k_layer_fused<NB, 8><<<CZ_FWG, 256, 0, st>>>(A); return;
-    }
+    if (A.pred_in)
+        launch_fused_spec<NB, true>(A, rw, st);
+    else
+        launch_fused_spec<NB, false>(A, rw, st);
 }
 
 // The layers [layer0, layer0 + n) (all fused_ok, one hidden size) as n
@@ -942,6 +959,20 @@ int chain_enqueue_fused(uint32_t layer0, uint32_t n, float *x_dev, float eps, fl
         A.gates_trace = gates_trace ? gates_trace + (uint64_t)p * L.d.topk : nullptr;
         A.pos = p;
         A.eps = eps;
+        // predicted experts: layer p + 1's top-k on layer p's router input
+        // (same expert count and top-k), in F.pred[(p + 1) % 2]
+        const LayerHost *Ln = p + 1 < n ? find_layer(layer0 + p + 1) : nullptr;
+        const LayerHost *Lp = p > 0 ? find_layer(layer0 + p - 1) : nullptr;
+        if (F.predict && Lp && Lp->d.experts == L.d.experts && Lp->d.topk == L.d.topk)
+            A.pred_in = F.pred + (uint64_t)(p % 2) * 64;
+        if (F.predict && Ln && Ln->d.experts == L.d.experts && Ln->d.topk == L.d.topk) {
+            A.pred_out = F.pred + (uint64_t)((p + 1) % 2) * 64;
+            A.rnext = Ln->router;
+            A.rbias_next = Ln->rbias;
+        }
+        A.lgpx = F.lgpx;
+        A.pred_mode = F.predict >= 2 ? (uint32_t)(F.predict - 1) : 0u;
+        A.pstat = F.pstat;
         const uint32_t rw = (uint32_t)((uint64_t)L.d.topk * L.d.inter / 1024);
         switch (H) {
             case 512: launch_fused_nb<8>(A, rw, st); break;
@@ -1123,7 +1154,7 @@ extern "C" void colizig_cuda_shutdown(void) {
         if (p) (void)hipFree(p);
     for (void *p : g.retired) (void)hipFree(p);
     for (void *p : {(void *)g.fused.r, (void *)g.fused.p, (void *)g.fused.zero, (void *)g.fused.lgx,
-                    (void *)g.fused.hx, (void *)g.fused.run})
+                    (void *)g.fused.hx, (void *)g.fused.run, (void *)g.fused.pred, (void *)g.fused.lgpx})
         if (p) (void)hipFree(p);
     if (g.fused.err_host) (void)hipHostFree(g.fused.err_host);
     StreamPool &P = g.pool;
@@ -3267,6 +3298,31 @@ extern "C" int colizig_hip_set_fused_decode(int enable) {
     const int prev = g.fused.enabled ? 1 : 0;
     g.fused.enabled = enable != 0;
     return prev;
+}
+
+// Predicted experts in the one-launch decode: 0 off, 1 on, 2 and 3 on with
+// the prediction spoiled on purpose (no slot keeps its prediction; slot 0
+// does not) so that every slot, or one, loads after the routing.  Returns
+// the previous setting, or -1 for another value.
+extern "C" int colizig_hip_set_fused_predict(int mode) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (mode < 0 || mode > 3) return -1;
+    const int prev = g.fused.predict;
+    g.fused.predict = mode;
+    return prev;
+}
+
+// Counts of the predicted experts since the last call: out[0] slots that had
+// a prediction, out[1] slots whose predicted expert was picked; then zeroes
+// them.  0, or -1 before any one-launch decode.
+extern "C" int colizig_hip_fused_predict_stats(uint64_t *out) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !g.fused.pstat || !out) return -1;
+    CZ_CHECK(hipStreamSynchronize(g.stream), -5);
+    CZ_CHECK(hipMemcpy(out, g.fused.pstat, 2 * sizeof(uint64_t), hipMemcpyDeviceToHost), -5);
+    CZ_CHECK(hipMemset(g.fused.pstat, 0, 2 * sizeof(uint64_t)), -5);
+    return 0;
 }
 
 extern "C" int colizig_hip_fused_decode_active(uint32_t layer0, uint32_t nlayers, int S) {

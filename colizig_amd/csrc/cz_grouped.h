@@ -70,8 +70,13 @@ struct GroupArgs {
     uint32_t *host_flag;
     uint32_t host_seq;
     uint32_t sgate_ready;      // 1: the RMS rows kernel already wrote sgate
-    unsigned long long *usage; // [E] routed-selection counters to bump, or null (a routing pass
-                               // whose picks another kernel routes and counts again)
+    unsigned long long *usage; // [E] routed-selection counters to bump, or null: k_route_tokens
+                               // bumps one counter per pick (one atomic each, for S = 1),
+                               // k_dispatch adds each expert's count of the round (one atomic
+                               // per routed expert, for S > 1: a hot expert picked by most
+                               // tokens would otherwise serialise hundreds of atomics on one
+                               // address); null in a routing pass whose picks another kernel
+                               // routes and counts again
 };
 
 // ---------------------------------------------------------------------------
@@ -243,7 +248,10 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
     __syncthreads();
     for (uint32_t e = tid; e <= E; e += blockDim.x) {
         G.offsets[e] = s_off[e];
-        if (e < E) G.counts[e] = s_cnt[e];
+        if (e < E) {
+            G.counts[e] = s_cnt[e];
+            if (G.usage && s_cnt[e]) atomicAdd(G.usage + e, (unsigned long long)s_cnt[e]);
+        }
     }
     const uint32_t nw = E * RS;  // bitmap words in use (<= CZ_DISPATCH_WORDS + CZ_MAX_E)
     for (uint32_t r0 = 0; r0 < SK; r0 += R) {

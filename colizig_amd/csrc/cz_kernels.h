@@ -655,15 +655,14 @@ __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
 // by DPP and readlane only.  Lane z < K leaves pick z in registers
 // (o_pos = z, o_id, o_gate) and writes s_idx[z] / s_gate[z] (LDS), which the
 // block reads after a barrier.  Must be called by a whole wave.
+// cz_route_wave_regs takes the logits in the wave's registers (v[m] in lane
+// l: expert l + 64m; overwritten), cz_route_wave_m reads them from lg.
 // ---------------------------------------------------------------------------
 template <int M>
-__device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
-                                       uint32_t *s_idx, float *s_gate, uint32_t &o_pos, uint32_t &o_id,
-                                       float &o_gate) {
+__device__ inline void cz_route_wave_regs(float (&v)[M], uint32_t E, uint32_t K, uint32_t norm_topk,
+                                          uint32_t *s_idx, float *s_gate, uint32_t &o_pos, uint32_t &o_id,
+                                          float &o_gate) {
     const uint32_t lane = cz_lane();
-    float v[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) v[m] = lg[min(lane + 64 * m, E - 1)];  // clamped: in bounds
     // moe.zig:439-440: mx = max over the logits (NaN-ignoring @max)
     float mx = -INFINITY;
 #pragma unroll
@@ -722,6 +721,16 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
         s_idx[lane] = o_id;
         s_gate[lane] = o_gate;
     }
+}
+
+template <int M>
+__device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
+                                       uint32_t *s_idx, float *s_gate, uint32_t &o_pos, uint32_t &o_id,
+                                       float &o_gate) {
+    float v[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) v[m] = lg[min(cz_lane() + 64 * m, E - 1)];  // clamped: in bounds
+    cz_route_wave_regs<M>(v, E, K, norm_topk, s_idx, s_gate, o_pos, o_id, o_gate);
 }
 
 // expert groups of 64 a routing wave holds for E experts

@@ -218,10 +218,9 @@ int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_d
 /* One-launch-per-layer decode.  colizig_hip_chain_decode and its graph run
  * a batch-1 chain of resident layers as one kernel per layer (plus one final
  * residual add per chain) when the device has 8 XCDs x 32 CUs and every layer
- * has no shared expert, hidden 512, 1024 or 2048, at most 128 experts and
- * K*I a multiple of 1024 with K*I/1024 in {1, 2, 4, 6, 8} and I a multiple
- * of K*I/32 (the Qwen3-30B-A3B shape and config 1 qualify); otherwise the
- * three-kernel decode.  Results are the same within the 1e-3 bar, routing
+ * has no shared expert, hidden 512, 1024 or 2048, at most 128 experts, K at
+ * most 32, I a multiple of 128 and K*I/1024 in {1, 2, 4, 6, 8} (the Qwen3-30B-A3B shape
+ * and config 1 qualify); otherwise the three-kernel decode.  Results are the same within the 1e-3 bar, routing
  * bit-identical.  colizig_hip_set_fused_decode(0) turns it off (returns the
  * previous setting); colizig_hip_fused_decode_active says whether a chain
  * would take it.  Its kernels exchange data between workgroups with bounded
@@ -230,6 +229,22 @@ int colizig_hip_chain_kernel_times(uint32_t layer0, uint32_t nlayers, float *x_d
  * layer launch and final-kernel mean durations (us_out[2]) from replayed
  * graphs of `reps` steps, x_dev advancing.  No counterpart in the reference. */
 int colizig_hip_set_fused_decode(int enable);
+
+/* Predicted experts in the one-launch decode (mode 1, the default): each
+ * layer's kernel also takes the next layer's top-k of its router logits on
+ * this layer's router input, and the next kernel requests those experts'
+ * rows before its own routing is known; a slot whose predicted expert was
+ * not picked loads the picked one after the routing.  Routing, gates and
+ * outputs are those of the layer's own routing either way.  0 turns it off;
+ * 2 and 3 spoil the prediction on purpose (no slot keeps its prediction;
+ * slot 0 does not) to exercise the late loads.  Returns the previous mode,
+ * -1 for a mode outside 0..3.  No counterpart in the reference. */
+int colizig_hip_set_fused_predict(int mode);
+
+/* Counts since the last call: out[0] slots that had a predicted expert,
+ * out[1] of them whose predicted expert was picked; then zeroes them.  0, or
+ * -1 before any one-launch decode ran.  No counterpart in the reference. */
+int colizig_hip_fused_predict_stats(uint64_t *out);
 
 /* The grouped regime's GEMMs (prefill, batch decode) on FP8 MFMA
  * (v_mfma_scale_f32_32x32x64_f8f6f4: E4M3 weights as they are, the A rows as

@@ -253,3 +253,58 @@ def test_one_launch_decode_graph_replay(gpu):
     hip.colizig_hip_graph_destroy(gh)
     xe.free()
     xg.free()
+
+
+@pytest.mark.parametrize("shape", ["tiny", "qwen3-30b"])
+def test_one_launch_decode_predicted_experts(gpu, oracle_lib, shape):
+    """The one-launch decode requests each layer's predicted experts (the
+    previous layer's kernel takes the next layer's top-k on its own router
+    input) before its routing.  With the prediction off, as computed, spoiled
+    (no slot keeps its prediction: every slot loads after the routing) and
+    half spoiled (slot 0 never keeps it): routing and gates equal bit for
+    bit, router inputs and the residual stream within 1e-5 relative L2 (only
+    the order of the down sums changes).  The hit counters count one
+    prediction per slot of every layer after the first; none is kept when
+    spoiled, slot 0's never when half spoiled."""
+    say(f"predicted experts, {shape}")
+    hip = _lib.hip()
+    if shape == "tiny":
+        H, E, K, I, nl, base = 512, 16, 4, 256, 5, 1700
+        for l in range(nl):
+            moe.register_layer(base + l, synth.make_layer(H, E, K, I, 0, True, seed=181 + l))
+    else:
+        H, E, K, I, nl, base = 2048, 128, 8, 768, 6, 1800
+        for l in range(nl):
+            moe.Layer.load(base + l, moe.dims(H, E, K, I), np.zeros((E, H), np.float32)).synth(seed=199 + l)
+    assert hip.colizig_hip_fused_decode_active(base, nl, 1) == 1
+    x0 = synth.hidden_states(1, H, seed=17)
+    st = np.zeros(2, np.uint64)
+    runs = {}
+    prev = hip.colizig_hip_set_fused_predict(1)
+    try:
+        for mode in (0, 1, 2, 3):
+            assert hip.colizig_hip_set_fused_predict(mode) >= 0
+            hip.colizig_hip_fused_predict_stats(st.ctypes.data)  # zero the counters
+            runs[mode] = _run_chain(hip, base, nl, x0, K)
+            assert hip.colizig_hip_fused_predict_stats(st.ctypes.data) == 0
+            if mode == 0:
+                assert st[0] == 0
+            else:
+                assert st[0] == (nl - 1) * K, st
+            if mode == 2:
+                assert st[1] == 0, st
+            if mode == 3:
+                assert st[1] <= (nl - 1) * (K - 1), st
+            say(f"  mode {mode}: predictions {int(st[0])}, picked {int(st[1])}")
+        assert hip.colizig_hip_set_fused_predict(4) == -1
+    finally:
+        hip.colizig_hip_set_fused_predict(prev)
+    x_ref, xn_ref, id_ref, g_ref = runs[0]
+    for mode in (1, 2, 3):
+        x, xn, idx, gates = runs[mode]
+        assert np.array_equal(idx, id_ref), f"mode {mode}: routing"
+        assert np.array_equal(f32_bits(gates[0]), f32_bits(g_ref[0])), f"mode {mode}: layer-0 gates"
+        assert np.max(np.abs(gates - g_ref) / g_ref) < 1e-5
+        assert rel_l2(xn, xn_ref) < 1e-5, f"mode {mode}: router inputs"
+        assert rel_l2(x, x_ref) < 1e-5, f"mode {mode}: x rel L2 {rel_l2(x, x_ref):.2e}"
+    say(f"  x rel L2 vs no prediction: " + ", ".join(f"{m}: {rel_l2(runs[m][0], x_ref):.1e}" for m in (1, 2, 3)))
