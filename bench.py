@@ -102,6 +102,8 @@ def main():
     ap.add_argument("--fused-predict", type=int, default=None, choices=[0, 1],
                     help="decode: request each layer's predicted experts before its routing (1, the library's "
                          "default) or after it (0)")
+    ap.add_argument("--attn-separate", action="store_true",
+                    help="attn: q, k and v as three launches (the reference's three calls) instead of one")
     ap.add_argument("--tokens", type=int, default=512, help="prefill tokens per step")
     ap.add_argument("--prefill-mfma", choices=["f16", "fp8"], default=None,
                     help="prefill/qwen4: the grouped GEMMs on f16 MFMA (weights widened, activations f16 hi + lo) "
@@ -579,8 +581,15 @@ def attn_bench(args) -> None:
 
     def token():
         for l in range(NL):
-            for role, (O, I) in enumerate(shapes):
-                moe.matmul_fp8_dev(ys[role].data_ptr(), x.data_ptr(), 1, I, O, moe.Fp8Matrix.attn_key(l, role), hs)
+            if args.attn_separate:
+                for role, (O, I) in enumerate(shapes):
+                    moe.matmul_fp8_dev(ys[role].data_ptr(), x.data_ptr(), 1, I, O, moe.Fp8Matrix.attn_key(l, role), hs)
+            else:  # q, k and v share their input: one launch; then o
+                moe.matmul_fp8_dev_multi([ys[r].data_ptr() for r in range(3)], x.data_ptr(), 1, H,
+                                         [shapes[r][0] for r in range(3)],
+                                         [moe.Fp8Matrix.attn_key(l, r) for r in range(3)], hs)
+                O, I = shapes[3]
+                moe.matmul_fp8_dev(ys[3].data_ptr(), x.data_ptr(), 1, I, O, moe.Fp8Matrix.attn_key(l, 3), hs)
 
     with torch.cuda.stream(st):
         token()
@@ -601,7 +610,9 @@ def attn_bench(args) -> None:
     us = e0.elapsed_time(e1) * 1000.0 / args.steps
     per_token = NL * sum(O * I + nblk(O) * nblk(I) * 4 for (O, I) in shapes)
     gbs = per_token / (us * 1e-6) / 1e9
-    log(f"attn: {NL} layers x q/k/v/o at batch 1: {us:.1f} us per token, {per_token / 1e6:.1f} MB, {gbs:.0f} GB/s")
+    launches = NL * (4 if args.attn_separate else 2)
+    log(f"attn: {NL} layers x q/k/v/o at batch 1 ({launches} launches): {us:.1f} us per token, "
+        f"{per_token / 1e6:.1f} MB, {gbs:.0f} GB/s")
     moe.set_vram_budget(0)
     print(json.dumps({
         "metric": "FP8 attention projections q/k/v/o at decode (keyed device GEMV), Qwen3-30B-A3B shape, 1 MI355X",
@@ -609,7 +620,8 @@ def attn_bench(args) -> None:
         "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "e4m3-weights/f32-accumulate", "data": "synthetic (seeded N(0,0.02) weights)",
         "config": {"workload": "qwen3-30b-a3b-attn-proj-decode", "layers": NL, "hidden": H, "q_dim": QD,
-                   "kv_dim": KVD, "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)"},
+                   "kv_dim": KVD, "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
+                   "qkv": "three launches" if args.attn_separate else "one launch (matmul_fp8_dev_multi)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole token, 192 launches"},
     }))

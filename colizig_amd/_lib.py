@@ -68,6 +68,7 @@ SIGNATURES = {
                                                ctypes.c_uint64]),
     "colizig_hip_matrix_load": (ctypes.c_int, [ctypes.c_uint64, vp, vp, ctypes.c_int, ctypes.c_int]),
     "colizig_hip_matmul_fp8_dev": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, vp]),
+    "colizig_hip_matmul_fp8_dev_multi": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp]),
     "colizig_hip_stream_usage": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]),
     "colizig_hip_usage_read": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]),
     "colizig_hip_usage_reset": (ctypes.c_int, []),

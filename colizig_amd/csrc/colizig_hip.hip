@@ -1313,6 +1313,24 @@ void launch_matmul_fp8(float *y, const float *x, const uint8_t *w, const float *
     }
 }
 
+template <int NB>
+void launch_gemv_fp8_multi(GemvMulti G, const float *x, int S, hipStream_t st) {
+    constexpr int ST = NB >= 32 ? 128 / NB : 4;
+    uint32_t b8 = 0;
+    for (uint32_t m = 0; m < G.n; ++m) b8 += (G.O[m] + 7) / 8;
+    const int rw = b8 >= (uint32_t)kGemvRows2Blocks ? 2 : 1;
+    uint32_t b = 0;
+    for (uint32_t m = 0; m < G.n; ++m) {
+        G.blk0[m] = b;
+        b += (G.O[m] + 4 * rw - 1) / (4 * rw);
+    }
+    G.blk0[G.n] = b;
+    if (rw == 2)
+        k_gemv_fp8_multi<NB, ST, 2><<<b, 256, 0, st>>>(G, x, (uint32_t)S);
+    else
+        k_gemv_fp8_multi<NB, ST, 1><<<b, 256, 0, st>>>(G, x, (uint32_t)S);
+}
+
 extern "C" int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
@@ -1429,6 +1447,58 @@ extern "C" int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int 
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(g_err, sizeof g_err, "matmul_fp8_dev launch: %s", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
+// Several keyed FP8 matrices of one row width on the same input rows in one
+// launch: y_devs[m][S][Os[m]] = x . dequant(W_keys[m])^T, each bit-identical
+// to colizig_hip_matmul_fp8_dev of that key alone (the same per-row kernel
+// body).  For a caller that has the q, k and v projections of a layer
+// together (attn.zig:206-208 makes them three matmulFp8Keyed calls): one
+// launch instead of three.  n in 1..4; every key resident as FP8 [Os[m]][I].
+extern "C" int colizig_hip_matmul_fp8_dev_multi(int n, float *const *y_devs, const uint64_t *keys, const int *Os,
+                                                const float *x_dev, int S, int I, void *stream) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || n < 1 || n > CZ_GEMV_MULTI || !y_devs || !keys || !Os || !x_dev || S < 1 || I < 1) return -1;
+    GemvMulti G{};
+    G.n = (uint32_t)n;
+    for (int m = 0; m < n; ++m) {
+        if (!y_devs[m] || Os[m] < 1 || !dev_aligned(x_dev, y_devs[m])) return -1;
+        const auto it = g.by_key.find(keys[m]);
+        if (keys[m] == 0 || it == g.by_key.end()) {
+            snprintf(g_err, sizeof g_err, "matmul_fp8_dev_multi: key %llu not resident", (unsigned long long)keys[m]);
+            return -7;
+        }
+        Slot &sl = g.slots[it->second];
+        if (sl.bf16 || sl.I != I || sl.O != Os[m]) {
+            snprintf(g_err, sizeof g_err, "matmul_fp8_dev_multi: key resident as %s %d x %d, called as FP8 %d x %d",
+                     sl.bf16 ? "BF16" : "FP8", sl.O, sl.I, Os[m], I);
+            return -1;
+        }
+        sl.clock = ++g.lru;
+        g.hits++;
+        G.y[m] = y_devs[m];
+        G.w[m] = (const uint8_t *)sl.w;
+        G.s[m] = (const float *)sl.s;
+        G.O[m] = (uint32_t)Os[m];
+    }
+    const hipStream_t st = pick_stream(stream);
+    switch ((I % 64) ? 0 : I / 64) {
+        case 4: launch_gemv_fp8_multi<4>(G, x_dev, S, st); break;
+        case 8: launch_gemv_fp8_multi<8>(G, x_dev, S, st); break;
+        case 16: launch_gemv_fp8_multi<16>(G, x_dev, S, st); break;
+        case 32: launch_gemv_fp8_multi<32>(G, x_dev, S, st); break;
+        case 48: launch_gemv_fp8_multi<48>(G, x_dev, S, st); break;
+        case 64: launch_gemv_fp8_multi<64>(G, x_dev, S, st); break;
+        default:  // another row width: one launch per matrix
+            for (int m = 0; m < n; ++m) launch_matmul_fp8(G.y[m], x_dev, G.w[m], G.s[m], S, I, Os[m], st);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "matmul_fp8_dev_multi launch: %s", hipGetErrorString(e));
         return -4;
     }
     return 0;

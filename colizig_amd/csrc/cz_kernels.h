@@ -937,13 +937,12 @@ __device__ inline float cz_row_dot(const uint32_t (&d)[NB / 4], const float (&x)
 // reaches every barrier).
 // ---------------------------------------------------------------------------
 template <int NB, int ST, int RW>
-__global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const float *__restrict__ x,
-                                                  const uint8_t *__restrict__ w, const float *__restrict__ scales,
-                                                  uint32_t S, uint32_t O) {
+__device__ __attribute__((always_inline)) inline void cz_gemv_fp8_block(
+    float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ w,
+    const float *__restrict__ scales, uint32_t S, uint32_t O, uint32_t blk, float4 *xs) {
     constexpr uint32_t I = 64 * NB, I4 = I / 4, NQ = (ST * I4 + 255) / 256;
-    __shared__ float4 xs[ST * I4];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t r0 = (blockIdx.x * 4 + wave) * RW;  // the wave's RW rows
+    const uint32_t r0 = (blk * 4 + wave) * RW;  // the wave's RW rows
     const uint32_t col0 = lane * NB;
     uint32_t d[RW][NB / 4];
     RowScales<NB> rs[RW];
@@ -974,6 +973,39 @@ __global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const f
         }
         __syncthreads();  // these tokens' readers are done before the next pass stores
     }
+}
+
+template <int NB, int ST, int RW>
+__global__ __launch_bounds__(256) void k_gemv_fp8(float *__restrict__ y, const float *__restrict__ x,
+                                                  const uint8_t *__restrict__ w, const float *__restrict__ scales,
+                                                  uint32_t S, uint32_t O) {
+    __shared__ float4 xs[ST * 16 * NB];
+    cz_gemv_fp8_block<NB, ST, RW>(y, x, w, scales, S, O, blockIdx.x, xs);
+}
+
+// Several keyed matrices of one row width on the same input rows in one
+// launch (the q, k and v projections of a layer): matrix m takes the
+// workgroups [blk0[m], blk0[m + 1]); each workgroup runs the single-matrix
+// GEMV's body on its matrix, so every output is bit-identical to a
+// k_gemv_fp8 launch of that matrix alone.
+#define CZ_GEMV_MULTI 4
+struct GemvMulti {
+    float *y[CZ_GEMV_MULTI];
+    const uint8_t *w[CZ_GEMV_MULTI];
+    const float *s[CZ_GEMV_MULTI];
+    uint32_t O[CZ_GEMV_MULTI];
+    uint32_t blk0[CZ_GEMV_MULTI + 1];
+    uint32_t n;
+};
+
+template <int NB, int ST, int RW>
+__global__ __launch_bounds__(256) void k_gemv_fp8_multi(GemvMulti G, const float *__restrict__ x, uint32_t S) {
+    __shared__ float4 xs[ST * 16 * NB];
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t k = 1; k < CZ_GEMV_MULTI; ++k)
+        if (k < G.n && blockIdx.x >= G.blk0[k]) m = k;
+    cz_gemv_fp8_block<NB, ST, RW>(G.y[m], x, G.w[m], G.s[m], S, G.O[m], blockIdx.x - G.blk0[m], xs);
 }
 
 // ---------------------------------------------------------------------------

@@ -90,6 +90,18 @@ def matmul_fp8_dev(y_ptr: int, x_ptr: int, S: int, I: int, O: int, key: int, str
     _check("colizig_hip_matmul_fp8_dev", _lib.hip().colizig_hip_matmul_fp8_dev(y_ptr, x_ptr, S, I, O, key, stream))
 
 
+def matmul_fp8_dev_multi(y_ptrs, x_ptr: int, S: int, I: int, Os, keys, stream=None) -> None:
+    """Several keyed FP8 matrices of row width I on the same input rows, one
+    launch: y_m[S,O_m] = x[S,I] @ dequant(W_keys[m])^T (asynchronous; the
+    bits of matmul_fp8_dev of each key)."""
+    n = len(keys)
+    ys = (ctypes.c_void_p * n)(*y_ptrs)
+    ks = (ctypes.c_uint64 * n)(*keys)
+    os_ = (ctypes.c_int * n)(*Os)
+    _check("colizig_hip_matmul_fp8_dev_multi",
+           _lib.hip().colizig_hip_matmul_fp8_dev_multi(n, ys, ks, os_, x_ptr, S, I, stream))
+
+
 def matrix_load_bf16(key: int, w_bits: np.ndarray) -> None:
     """Puts BF16 rows w[O,I] (uint16 bits) under `key` in the HBM cache."""
     w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)

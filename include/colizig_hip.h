@@ -80,6 +80,18 @@ int colizig_cuda_matmul_fp8(float *y, const float *x, const unsigned char *w, co
 int colizig_hip_matrix_load(uint64_t key, const unsigned char *w, const float *scales, int I, int O);
 int colizig_hip_matmul_fp8_dev(float *y_dev, const float *x_dev, int S, int I, int O, uint64_t key, void *stream);
 
+/* Several keyed FP8 matrices of one row width I on the same input rows x_dev
+ * [S][I] in one launch: y_devs[m] [S][Os[m]] = x . dequant(W_keys[m])^T,
+ * each bit-identical to colizig_hip_matmul_fp8_dev of that key alone.  For a
+ * caller that has a layer's q, k and v projections together (the reference
+ * makes them three matmulFp8Keyed calls, qwen3moe/attn.zig:206-208): one
+ * launch instead of three; the 1 MiB k and v matrices are launch-bound on
+ * their own.  n in 1..4, every key resident as FP8 [Os[m]][I].  Returns 0,
+ * -1 bad arguments or a key resident with another shape or type, -7 a key
+ * not resident, -4 launch failed.  No counterpart in the reference. */
+int colizig_hip_matmul_fp8_dev_multi(int n, float *const *y_devs, const uint64_t *keys, const int *Os,
+                                     const float *x_dev, int S, int I, void *stream);
+
 /* BF16 rows (lm_head and the other BF16 NativeMatrix GEMVs: dotBf16,
  * src/ops/matmul.zig:84-110; tensors.zig's NativeMatrix(bf16).matmul) on
  * device activations: colizig_hip_matrix_load_bf16 puts w [O][I] (BF16 bits)

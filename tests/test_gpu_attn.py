@@ -6,6 +6,7 @@ relative L2 1e-5 (the same per-128-block partial sums as the decode kernels;
 the oracle sums every product in order)."""
 from __future__ import annotations
 
+import ctypes
 import sys
 
 import numpy as np
@@ -125,3 +126,53 @@ def test_matmul_dev_errors(gpu):
         moe.set_vram_budget(0)
         xb.free()
         yb.free()
+
+
+@pytest.mark.parametrize("S", [1, 5])
+def test_qkv_in_one_launch(gpu, oracle_lib, S):
+    """colizig_hip_matmul_fp8_dev_multi: a layer's q, k and v projections on
+    the same input rows in one launch give, for each matrix, the bits of its
+    own colizig_hip_matmul_fp8_dev call, and the oracle's matmulFp8 to the
+    bar.  Also a row width off the 128-bit path (one launch per matrix
+    there) and the argument checks."""
+    say(f"q/k/v in one launch S={S}")
+    hip = _lib.hip()
+    moe.set_vram_budget(1 << 30)
+    rng = np.random.default_rng(300 + S)
+    bufs = []
+    try:
+        for I, Os in ((H, (QD, KVD, KVD)), (200, (130, 7))):
+            mats, keys = [], []
+            for role, O in enumerate(Os):
+                w, s = synth.block_quantize(rng.normal(0, 0.02, size=(O, I)).astype(np.float32))
+                key = moe.Fp8Matrix.attn_key(21 if I == H else 22, role)
+                moe.matrix_load(key, w, s)
+                mats.append((w, s))
+                keys.append(key)
+            x = rng.normal(size=(S, I)).astype(np.float32)
+            xb = moe.DeviceBuffer(x.nbytes)
+            xb.upload(x)
+            ybs = [moe.DeviceBuffer(S * O * 4) for O in Os]
+            bufs += [xb] + ybs
+            moe.matmul_fp8_dev_multi([b.ptr for b in ybs], xb.ptr, S, I, Os, keys)
+            assert hip.colizig_hip_sync() == 0
+            for m, O in enumerate(Os):
+                y = ybs[m].download(np.empty((S, O), np.float32))
+                single = _dev_matmul(x, keys[m], I, O)
+                assert np.array_equal(f32_bits(y), f32_bits(single)), f"I={I} matrix {m}: bits"
+                ref = oracle_lib.matmul_fp8(x, mats[m][0], mats[m][1], S, I, O)
+                assert rel_l2(y, ref) < RTOL_L2
+        # argument checks: too many matrices, a key not resident, a shape other than the resident one
+        y3 = (ctypes.c_void_p * 5)(*([bufs[1].ptr] * 5))
+        k3 = (ctypes.c_uint64 * 5)(*([keys[0]] * 5))
+        o3 = (ctypes.c_int * 5)(*([130] * 5))
+        assert hip.colizig_hip_matmul_fp8_dev_multi(5, y3, k3, o3, bufs[0].ptr, 1, 200, None) == -1
+        k3[0] = 0xDEADBEEF
+        assert hip.colizig_hip_matmul_fp8_dev_multi(1, y3, k3, o3, bufs[0].ptr, 1, 200, None) == -7
+        k3[0] = keys[0]
+        o3[0] = 131
+        assert hip.colizig_hip_matmul_fp8_dev_multi(1, y3, k3, o3, bufs[0].ptr, 1, 200, None) == -1
+    finally:
+        moe.set_vram_budget(0)
+        for b in bufs:
+            b.free()
