@@ -308,3 +308,54 @@ def test_one_launch_decode_predicted_experts(gpu, oracle_lib, shape):
         assert rel_l2(xn, xn_ref) < 1e-5, f"mode {mode}: router inputs"
         assert rel_l2(x, x_ref) < 1e-5, f"mode {mode}: x rel L2 {rel_l2(x, x_ref):.2e}"
     say(f"  x rel L2 vs no prediction: " + ", ".join(f"{m}: {rel_l2(runs[m][0], x_ref):.1e}" for m in (1, 2, 3)))
+
+
+def test_one_launch_decode_ties_and_nan_routers(gpu, oracle_lib):
+    """Predicted experts where the routing is least regular: a layer whose
+    router has four identical rows (exact ties: the lowest id wins) and a
+    layer whose router rows are NaN but for experts 0 and 1 (two valid
+    experts for top-4: the scan's remaining picks are expert 0, twice, and so
+    are the predicted ones).  With the prediction on, off, spoiled and half
+    spoiled, and on the three-kernel decode: the same routing and gates bit
+    for bit, and every layer's routing equals the oracle's on the GPU's own
+    router input."""
+    say("one-launch decode: ties and NaN router rows")
+    hip = _lib.hip()
+    H, E, K, I, nl, base = 512, 16, 4, 256, 4, 1900
+    hosts = [synth.make_layer(H, E, K, I, 0, True, seed=211 + l) for l in range(nl)]
+    r1 = hosts[1]["router"].copy()
+    r1[3] = r1[4] = r1[5] = r1[2]
+    hosts[1]["router"] = r1
+    r2 = hosts[2]["router"].copy()
+    r2[2:] = np.nan
+    hosts[2]["router"] = r2
+    for l in range(nl):
+        moe.register_layer(base + l, hosts[l])
+    assert hip.colizig_hip_fused_decode_active(base, nl, 1) == 1
+    orcs = [oracle_lib.OracleLayer(h) for h in hosts]
+    x0 = synth.hidden_states(1, H, seed=23)
+    runs = {}
+    prev = hip.colizig_hip_set_fused_predict(1)
+    try:
+        for mode in (1, 0, 2, 3):
+            hip.colizig_hip_set_fused_predict(mode)
+            runs[mode] = _run_chain(hip, base, nl, x0, K)
+    finally:
+        hip.colizig_hip_set_fused_predict(prev)
+    fprev = hip.colizig_hip_set_fused_decode(0)
+    try:
+        runs["three"] = _run_chain(hip, base, nl, x0, K)
+    finally:
+        hip.colizig_hip_set_fused_decode(fprev)
+    x1, xn1, id1, g1 = runs[1]
+    assert list(id1[2][2:]) == [0, 0], id1[2]  # two valid experts: expert 0 fills the rest
+    for l in range(nl):
+        ri, rg, _ = orcs[l].route(xn1[l])
+        assert np.array_equal(id1[l], ri), f"layer {l}: routing vs the oracle's"
+        assert np.array_equal(f32_bits(g1[l]), f32_bits(rg)), f"layer {l}: gates vs the oracle's"
+    for key, (x, xn, idx, gates) in runs.items():
+        assert np.array_equal(idx, id1), f"{key}: routing"
+        assert np.array_equal(f32_bits(gates[0]), f32_bits(g1[0])), f"{key}: layer-0 gates"
+        assert np.all(np.isfinite(x)), f"{key}: x"
+        assert rel_l2(x, x1) < 1e-5, f"{key}: x rel L2 {rel_l2(x, x1):.2e}"
+    say(f"  picks of the NaN layer {id1[2].tolist()}; tied layer {id1[1].tolist()}")
