@@ -248,7 +248,7 @@ struct Ctx {
     int64_t next_handle = 1;
     StreamPool pool;
     FusedState fused;
-    bool prefill_fp8 = false;  // grouped GEMMs on FP8 MFMA (k_gg8) instead of f16 (k_gg)
+    bool prefill_fp8 = true;   // grouped GEMMs on FP8 MFMA (k_gg8), else f16 (k_gg)
 };
 
 Ctx g;
@@ -402,6 +402,15 @@ enum Which { kRouter = 1, kUp = 2, kDown = 4, kAll = 7 };
 
 // The RMS rows kernel that launch_router runs for these arguments also forms
 // the shared-expert gate (the workgroup-per-row form, with a shared expert).
+// Whether the RMS rows of S tokens go through k_rms_rows_wg (launch_router's
+// choice), which can also write xn's FP8-MFMA terms.
+bool rms_rows_wg(const LayerHost &Lh, int S) {
+    const colizig_dims &d = Lh.d;
+    const uint32_t q = (d.hidden / 4 + 255) / 256;
+    if (Lh.router_bf16) return d.hidden % 256 == 0 && (q == 1 || q == 2 || q == 4 || q == 8);
+    return S >= kGroupedMinTokens && d.hidden % 256 == 0 && q <= 8;
+}
+
 bool rms_rows_write_sgate(const StepArgs &A) {
     const LayerDev &L = A.L;
     return A.rms && A.S >= kGroupedMinTokens && L.H % 256 == 0 && L.SI != 0 && (L.H / 4 + 255) / 256 <= 8;
@@ -696,6 +705,11 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         A.xh = w.xh;
         A.xl = w.xl;
     }
+    const bool xq_rms = rms && f8 && rms_rows_wg(Lh, S);
+    if (xq_rms) {  // ... or its three E4M3 terms
+        A.xq = w.xq;
+        A.xe = w.xe;
+    }
     launch_router(A, st);
     if (Lh.shn_dtype >= 0) {
         if (int rc = launch_shared_native_pre(Lh, rms ? w.xn : x, S, st)) return rc;
@@ -746,7 +760,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         const uint64_t n = rows * (K / 32);
         k_quant3<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(src, (uint32_t)rows, K, q, rows * K, e, rows * K / 32);
     };
-    if (f8) quant3(G.xn, (uint64_t)S, L.H, w.xq, w.xe);
+    if (f8 && !xq_rms) quant3(G.xn, (uint64_t)S, L.H, w.xq, w.xe);  // no RMS rows kernel splits x
     // gate/up
     GGProblem P{};
     P.w0 = L.ew;
@@ -797,6 +811,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         quant3(w.h, sk, L.I, w.hq, w.he);
         if (L.SI) quant3(w.hs, (uint64_t)S, L.SI, w.hsq, w.hse);
     }
+
     // down
     GGProblem D{};
     D.w0 = L.ew + 2ull * L.I * L.H;

@@ -334,7 +334,7 @@ struct GGProblem {
     int routed;             // 1: tiles from the dispatch table; 0: shared (rows = tokens in order)
     uint32_t rows_total;    // shared: S
     // FP8-MFMA form (k_gg8): A rows as three E4M3 terms with E8M0 exponents
-    // per 32 columns (cz_quant3); GATEUP writes h as f32 rows to c
+    // per 32 columns (cz_q3_scale); GATEUP writes h as f32 rows to c
     const uint8_t *aq;      // [3][rows][Kd] (term planes aq_plane bytes apart)
     const uint8_t *ae;      // [3][rows][Kd/32] (planes ae_plane bytes apart)
     uint64_t aq_plane, ae_plane;
@@ -631,15 +631,8 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem PR, GGProb
 // ---------------------------------------------------------------------------
 
 // E4M3 of v (|v| <= 448), round to nearest even; byte in the low 8 bits.
-__device__ __forceinline__ uint32_t cz_f32_to_e4m3(float v) {
-    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xffu;
-}
-
-// Rows of K columns (K % 32 == 0) to three E4M3 terms: one thread per 32
-// columns of a row.  Term t: k_t = the least k with max|r_t| <= 448 * 2^k
-// over the group (r_0 = x), q_t = e4m3(r_t * 2^-k_t), r_{t+1} = r_t -
-// 2^k_t * q_t (exact: q_t rounds r_t * 2^-k_t); exponent byte k_t + 127, or
-// 0 with q_t = 0 for an all-zero group.
+// Rows of K columns (K % 32 == 0) to three E4M3 terms (cz_q3_scale): one
+// thread per 32 columns of a row.  For inputs no producing kernel splits.
 __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, uint32_t rows, uint32_t K,
                                                uint8_t *__restrict__ q, uint64_t q_plane, uint8_t *__restrict__ e,
                                                uint64_t e_plane) {
@@ -659,38 +652,19 @@ __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, u
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) amax = fmaxf(amax, __builtin_fabsf(r[i]));
-        int k = 0;
-        uint32_t eb = 0;
-        if (amax > 0.0f) {
-            const int ef = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xffu);
-            k = (ef ? ef - 127 : -127) - 8;  // floor(log2 amax) - 8 (subnormals: below -127)
-            if (amax > __builtin_ldexpf(448.0f, k)) ++k;
-            k = max(-126, min(k, 127));
-            eb = (uint32_t)(k + 127);
-        }
-        const float inv = amax > 0.0f ? __builtin_ldexpf(1.0f, -k) : 0.0f;
-        const float sc = amax > 0.0f ? __builtin_ldexpf(1.0f, k) : 0.0f;
+        const CzQ3 sc = cz_q3_scale(amax);
         uint32_t w[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             uint32_t word = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t b = amax > 0.0f ? cz_f32_to_e4m3(r[4 * i + j] * inv) : 0u;
-                word |= b << (8 * j);
-            }
+            for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[4 * i + j], sc) << (8 * j);
             w[i] = word;
-#pragma unroll
-            for (int j = 0; j < 4; j += 2) {
-                const cz_float2 d = j ? cz_fp8x2_hi(word) : cz_fp8x2_lo(word);
-                r[4 * i + j] = r[4 * i + j] - d.x * sc;
-                r[4 * i + j + 1] = r[4 * i + j + 1] - d.y * sc;
-            }
         }
         uint4 *qo = reinterpret_cast<uint4 *>(q + t * q_plane + row * K + grp * 32);
         qo[0] = make_uint4(w[0], w[1], w[2], w[3]);
         qo[1] = make_uint4(w[4], w[5], w[6], w[7]);
-        e[t * e_plane + row * ng + grp] = (uint8_t)eb;
+        e[t * e_plane + row * ng + grp] = (uint8_t)sc.eb;
     }
 }
 

@@ -116,6 +116,8 @@ struct StepArgs {
     float *gates_trace;    // nullable [S][K]
     float *xn_trace;       // nullable [S][H]
     _Float16 *xh, *xl;     // nullable [S][H]: k_rms_rows also writes xn as f16 hi + lo (xn ~= hi + lo)
+    uint8_t *xq, *xe;      // nullable: k_rms_rows_wg also writes xn as three E4M3 terms [3][S][H] with
+                           // E8M0 exponents per 32 columns [3][S][H/32] (cz_q3_scale), the FP8-MFMA A rows
     int S;
     int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
     int rms;
@@ -392,6 +394,36 @@ __device__ __forceinline__ void cz_rms_store(const StepArgs &A, uint64_t o, floa
     }
 }
 
+// Activations for the FP8-MFMA grouped GEMMs: each 32-column group of a row
+// as three E4M3 terms.  Term t of a group with max |r_t| = amax: k_t = the
+// least k with amax <= 448 * 2^k (clamped to [-126, 127]), q_t = e4m3(r_t *
+// 2^-k_t), r_{t+1} = r_t - 2^k_t * q_t (exact: q_t rounds r_t * 2^-k_t), the
+// exponent byte k_t + 127; an all-zero group has byte 0 and zero terms.
+__device__ __forceinline__ uint32_t cz_f32_to_e4m3(float v) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xffu;
+}
+
+struct CzQ3 {
+    float inv, sc;  // 2^-k, 2^k (0 for an all-zero group)
+    uint32_t eb;    // exponent byte
+};
+
+__device__ __forceinline__ CzQ3 cz_q3_scale(float amax) {
+    if (!(amax > 0.0f)) return CzQ3{0.0f, 0.0f, 0u};
+    const int ef = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xffu);
+    int k = (ef ? ef - 127 : -127) - 8;  // floor(log2 amax) - 8 (subnormals: below -127)
+    if (amax > __builtin_ldexpf(448.0f, k)) ++k;
+    k = max(-126, min(k, 127));
+    return CzQ3{__builtin_ldexpf(1.0f, -k), __builtin_ldexpf(1.0f, k), (uint32_t)(k + 127)};
+}
+
+// e4m3 byte of r in the group's scale, and r less what the byte represents
+__device__ __forceinline__ uint32_t cz_q3_term(float &r, const CzQ3 &s) {
+    const uint32_t b = s.eb ? cz_f32_to_e4m3(r * s.inv) : 0u;
+    r = r - cz_fp8x2_lo(b).x * s.sc;
+    return b;
+}
+
 // One workgroup of 256 threads per token row (H % 256 == 0, H <= 1024 Q):
 // the row is requested at once as 128-bit loads (Q per thread) and staged in
 // LDS; wave 0 forms the f64 sum of squares (cz_rms_inv), every thread then
@@ -458,6 +490,24 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
                                  (_Float16)(y.z - (float)hi[2]), (_Float16)(y.w - (float)hi[3])};
             reinterpret_cast<cz_half4 *>(A.xh + row)[q] = hi;
             reinterpret_cast<cz_half4 *>(A.xl + row)[q] = lo;
+        }
+        if (A.xq) {  // the group of 32 columns is 8 consecutive lanes (H % 32 == 0: whole groups active)
+            float r[4] = {y.x, y.y, y.z, y.w};
+            const uint64_t qp = (uint64_t)A.S * H, ep = (uint64_t)A.S * (H / 32);
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                float am = fmaxf(fmaxf(__builtin_fabsf(r[0]), __builtin_fabsf(r[1])),
+                                 fmaxf(__builtin_fabsf(r[2]), __builtin_fabsf(r[3])));
+                am = fmaxf(am, cz_dpp<0xB1>(am));   // lanes xor 1
+                am = fmaxf(am, cz_dpp<0x4E>(am));   // xor 2
+                am = fmaxf(am, cz_dpp<0x141>(am));  // the mirror within 8: every lane of the 8
+                const CzQ3 sc = cz_q3_scale(am);
+                uint32_t word = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[j], sc) << (8 * j);
+                reinterpret_cast<uint32_t *>(A.xq + t * qp + row)[q] = word;
+                if ((q & 7u) == 0) A.xe[t * ep + (uint64_t)blockIdx.x * (H / 32) + q / 8] = (uint8_t)sc.eb;
+            }
         }
     }
 }

@@ -11,6 +11,16 @@ import pytest
 from colizig_amd import _lib, moe, synth
 from tests.helpers import f32_bits, rel_l2
 
+
+@pytest.fixture(autouse=True)
+def mfma_mode(gpu):
+    """These cases run the grouped GEMMs on f16 MFMA (test_gpu_prefill_fp8.py
+    runs them again on FP8 MFMA, the library's default)."""
+    hip = _lib.hip()
+    prev = hip.colizig_hip_set_prefill_fp8(0)
+    yield
+    hip.colizig_hip_set_prefill_fp8(prev)
+
 pytestmark = pytest.mark.gpu
 
 RTOL_L2 = 1e-3

@@ -14,8 +14,21 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(autouse=True)
-def fp8_mode(gpu):
+def mfma_mode(gpu):  # shadows test_gpu_grouped's f16 fixture of the same name
     hip = _lib.hip()
     prev = hip.colizig_hip_set_prefill_fp8(1)
     yield
     hip.colizig_hip_set_prefill_fp8(prev)
+
+
+@pytest.mark.parametrize("SI", [0, 256])
+def test_fp8_chain_vs_oracle_chain(gpu, oracle_lib, SI):
+    """The chained grouped regime on FP8 MFMA, where the RMS rows kernel writes
+    the gate/up GEMM's E4M3 terms of xn (with and without a shared expert):
+    3 layers x 2 steps of 20 tokens against the oracle's own chain from the
+    same x0 (routing bit-exact on the GPU's router inputs and against the
+    oracle chain's picks, router inputs and residual stream within 1e-3)."""
+    from colizig_amd import synth
+    from tests.test_gpu_chain import chain_vs_oracle
+    hosts = [synth.make_layer(512, 16, 4, 256, SI, True, seed=331 + l + SI) for l in range(3)]
+    chain_vs_oracle(oracle_lib, hosts, 2100 + SI, 20, tokens=2, seed=5, label=f"fp8 chain SI={SI}")
