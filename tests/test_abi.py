@@ -76,6 +76,39 @@ def test_no_device_error_paths():
     assert [a.value for a in v] == [0, 0, 0, 0]
     h.colizig_cuda_shutdown()  # safe when not initialised
     assert h.colizig_hip_malloc(1024) is None
+    # the multi-matrix GEMV and the prediction counters refuse before init
+    ys = (ctypes.c_void_p * 1)(p(y).value)
+    ks = (ctypes.c_uint64 * 1)(1)
+    os_ = (ctypes.c_int * 1)(4)
+    assert h.colizig_hip_matmul_fp8_dev_multi(1, ys, ks, os_, p(x), 1, 4, None) == -1
+    st = np.zeros(2, np.uint64)
+    assert h.colizig_hip_fused_predict_stats(p(st)) == -1
+
+
+def test_host_side_switches():
+    """Mode switches that are host state only: each returns the previous
+    setting and refuses a value outside its range (no device needed)."""
+    h = _lib.hip()
+    prev = h.colizig_hip_set_fused_predict(0)
+    assert prev in (0, 1, 2, 3)
+    try:
+        assert h.colizig_hip_set_fused_predict(3) == 0
+        assert h.colizig_hip_set_fused_predict(4) == -1
+        assert h.colizig_hip_set_fused_predict(-1) == -1
+        assert h.colizig_hip_set_fused_predict(1) == 3
+    finally:
+        h.colizig_hip_set_fused_predict(prev)
+    p8 = h.colizig_hip_set_prefill_fp8(0)
+    try:
+        assert h.colizig_hip_set_prefill_fp8(1) == 0
+        assert h.colizig_hip_set_prefill_fp8(0) == 1
+    finally:
+        h.colizig_hip_set_prefill_fp8(p8)
+    fd = h.colizig_hip_set_fused_decode(0)
+    try:
+        assert h.colizig_hip_set_fused_decode(1) == 0
+    finally:
+        h.colizig_hip_set_fused_decode(fd)
 
 
 def test_loader_falls_back_without_device():
