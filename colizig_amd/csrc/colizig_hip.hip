@@ -173,6 +173,7 @@ struct StreamPool {
     int predict_mode = 2;
     float *pred_logits = nullptr, *pred_gates = nullptr, *pred_sgate = nullptr;
     uint32_t *pred_idx = nullptr, *pred_tord = nullptr;
+    uint32_t *route_count = nullptr;  // the router kernel's block counter (one-token routing), kept at zero
     uint32_t *h_pred = nullptr, *h_pflag = nullptr;
     uint32_t pseq = 0;
     std::unordered_map<uint32_t, std::vector<uint32_t>> pred_ids;  // layer -> its next-layer prediction
@@ -1175,7 +1176,7 @@ extern "C" void colizig_cuda_shutdown(void) {
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
     for (void *p : {(void *)P.base, (void *)P.pred_logits, (void *)P.pred_gates, (void *)P.pred_sgate,
-                    (void *)P.pred_idx, (void *)P.pred_tord, (void *)P.tok_logits, (void *)P.tok_gates,
+                    (void *)P.pred_idx, (void *)P.pred_tord, (void *)P.route_count, (void *)P.tok_logits, (void *)P.tok_gates,
                     (void *)P.tok_idx, (void *)P.tok_tord, (void *)P.tok_ptr_dev})
         if (p) (void)hipFree(p);
     for (void *p : {(void *)P.h_idx, (void *)P.h_flag, (void *)P.h_pred, (void *)P.h_pflag, (void *)P.h_tok,
@@ -2584,7 +2585,29 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     StreamPool &P = g.pool;
     Work &w = g.work;
     const StepArgs A = step_args(L, x, S, out, rms, eps, xres, nullptr, nullptr, nullptr);
-    launch_router(A, st);
+    // one token: the picks go into host memory, then a sequence number; the
+    // host waits on that (no copy, no event).  The router kernel's last block
+    // routes where the router is k_router_fast and E <= 128; otherwise a
+    // routing launch follows the router.
+    const bool direct = S == 1;
+    const uint32_t hw = L.d.hidden % 32 ? 0u : L.d.hidden / 32;
+    const bool route_in_router = direct && !L.router_bf16 && L.d.experts <= 128 &&
+                                 (hw == 8 || hw == 16 || hw == 32 || hw == 64 || hw == 96 || hw == 128);
+    void *h_idx_dev = nullptr, *h_flag_dev = nullptr;
+    if (direct) {
+        CZ_CHECK(hipHostGetDevicePointer(&h_idx_dev, P.h_idx, 0), -4);
+        CZ_CHECK(hipHostGetDevicePointer(&h_flag_dev, P.h_flag, 0), -4);
+    }
+    if (route_in_router) {
+        StepArgs Ar = A;
+        Ar.route_count = P.route_count;
+        Ar.host_idx = (uint32_t *)h_idx_dev;
+        Ar.host_flag = (uint32_t *)h_flag_dev;
+        Ar.host_seq = ++P.seq;
+        launch_router(Ar, st);
+    } else {
+        launch_router(A, st);
+    }
     GroupArgs G{};
     G.L = A.L;
     G.S = S;
@@ -2598,18 +2621,14 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     G.usage = nullptr;  // the expert kernels below route again and count
     G.xh = nullptr;  // routing only: the grouped regime below splits x itself
     G.xl = nullptr;
-    // one token: the routing kernel writes the picks into host memory and then
-    // a sequence number; the host waits on that (no copy, no event)
-    const bool direct = S == 1;
-    if (direct) {
-        void *di = nullptr, *df = nullptr;
-        CZ_CHECK(hipHostGetDevicePointer(&di, P.h_idx, 0), -4);
-        CZ_CHECK(hipHostGetDevicePointer(&df, P.h_flag, 0), -4);
-        G.host_idx = (uint32_t *)di;
-        G.host_flag = (uint32_t *)df;
-        G.host_seq = ++P.seq;
+    if (!route_in_router) {
+        if (direct) {
+            G.host_idx = (uint32_t *)h_idx_dev;
+            G.host_flag = (uint32_t *)h_flag_dev;
+            G.host_seq = ++P.seq;
+        }
+        for_route_groups(A.L.E, [&](auto m) { launch_route_tokens<decltype(m)::value>(G, st); });
     }
-    for_route_groups(A.L.E, [&](auto m) { launch_route_tokens<decltype(m)::value>(G, st); });
     const bool predict = direct && (P.predict_mode & 1) && next && next->streamed() && next->ready() &&
                          next->d.hidden == L.d.hidden && next->d.topk <= CZ_MAX_K;
     if (predict) {
@@ -2683,7 +2702,7 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     const size_t nk = (size_t)S * L.d.topk;
     CZ_CHECK(hipGetLastError(), -4);
     if (direct) {
-        if (int rc = wait_host_seq(P.h_flag, G.host_seq, st, "routing read-back")) return rc;
+        if (int rc = wait_host_seq(P.h_flag, P.seq, st, "routing read-back")) return rc;
     } else {
         CZ_CHECK(hipMemcpyAsync(P.h_idx, w.idx, nk * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
         CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
@@ -2794,7 +2813,8 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
          hipMalloc(&P.pred_idx, CZ_MAX_K * sizeof(uint32_t)) != hipSuccess ||
          hipMalloc(&P.pred_gates, CZ_MAX_K * sizeof(float)) != hipSuccess ||
          hipMalloc(&P.pred_sgate, 64) != hipSuccess ||
-         hipMalloc(&P.pred_tord, CZ_MAX_K * sizeof(uint32_t)) != hipSuccess))
+         hipMalloc(&P.pred_tord, CZ_MAX_K * sizeof(uint32_t)) != hipSuccess ||
+         hipMalloc(&P.route_count, sizeof(uint32_t)) != hipSuccess || hipMemset(P.route_count, 0, 4) != hipSuccess))
         return -2;
     if (!P.copy) {
         CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);

@@ -118,6 +118,11 @@ struct StepArgs {
     _Float16 *xh, *xl;     // nullable [S][H]: k_rms_rows also writes xn as f16 hi + lo (xn ~= hi + lo)
     uint8_t *xq, *xe;      // nullable: k_rms_rows_wg also writes xn as three E4M3 terms [3][S][H] with
                            // E8M0 exponents per 32 columns [3][S][H/32] (cz_q3_scale), the FP8-MFMA A rows
+    // nullable: k_router_fast at S = 1, E <= 128 also routes the token in its
+    // last workgroup (route_count: a zeroed device counter it leaves zeroed)
+    // and writes the picks to host_idx, then host_seq to host_flag
+    uint32_t *route_count, *host_idx, *host_flag;
+    uint32_t host_seq;
     int S;
     int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
     int rms;
@@ -285,9 +290,18 @@ __device__ __forceinline__ void cz_router_stage_row(const StepArgs &A, float *sm
     }
 }
 
+template <int M>
+__device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E, uint32_t K, uint32_t norm_topk,
+                                       uint32_t *s_idx, float *s_gate, uint32_t &o_pos, uint32_t &o_id,
+                                       float &o_gate);
+
 // One wave per block, two experts per wave (one per half).  NS = H/32: every
 // router element the lane needs is loaded into registers before the input
-// tile is staged and the chains run.
+// tile is staged and the chains run.  With A.host_flag (one token, E <= 128)
+// the last block to finish routes the token (the routing wave of the decode
+// kernels on the logits, after an agent-scope fence on both sides of the
+// block counter) and hands the picks to the host, in place of a routing
+// launch.
 template <int NS>
 __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
     constexpr uint32_t H = 32 * NS;
@@ -335,6 +349,29 @@ __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
         float lg = cz_router_combine(acc, j, hb);
         if (A.L.router_bias) lg = lg + A.L.router_bias[ec];
         if (j == 0 && e < E) A.logits[(uint64_t)(t0 + t) * E + e] = lg;
+    }
+    if (A.host_flag) {  // uniform
+        __shared__ uint32_t s_last;
+        __shared__ uint32_t s_ri[CZ_MAX_K];
+        __shared__ float s_rg[CZ_MAX_K];
+        __threadfence();  // this block's logits are visible to the last block
+        if (threadIdx.x == 0) s_last = atomicAdd(A.route_count, 1u) == gridDim.x * gridDim.y - 1u ? 1u : 0u;
+        __syncthreads();
+        if (s_last) {
+            __threadfence();  // every block's logits are visible here
+            uint32_t o_pos = 0, o_id = 0;
+            float o_gate = 0.0f;
+            if (E <= 64)  // the routing launch's wave for E experts (cz_route_groups)
+                cz_route_wave_m<1>(A.logits, E, A.L.K, A.L.norm_topk, s_ri, s_rg, o_pos, o_id, o_gate);
+            else
+                cz_route_wave_m<2>(A.logits, E, A.L.K, A.L.norm_topk, s_ri, s_rg, o_pos, o_id, o_gate);
+            if (lane < A.L.K) A.host_idx[o_pos] = o_id;  // in pick order
+            __threadfence_system();
+            if (lane == 0) {
+                *A.route_count = 0u;  // for the next launch (stream order)
+                __hip_atomic_store(A.host_flag, A.host_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
     }
 }
 
