@@ -535,72 +535,83 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     }
     cz_lds_wait(&s_stage, 2u, A.err);  // the slots' experts and the gates are known
     routed = true;
-    {
-        const uint32_t rl = s_rl;
-        bool any = false;
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-            if ((rl >> zr[r]) & 1u) {
-                slr[r] = cz_slot(L, min(s_idx[s_fp[zr[r]]], E - 1));
-                any = true;
-            }
-        if (any) {
-            load_scales();
-            load_down_scale();
-        }
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-            if ((rl >> zr[r]) & 1u) load_row(r);
-#pragma unroll
-        for (int i = 0; i < RW; ++i)
-            if ((rl >> zr[i]) & 1u) load_down(i);
-    }
-    float gz[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) gz[r] = s_gate[s_fp[zr[r]]];
-    // ---- the scales to the lanes that use them
-#pragma unroll
-    for (uint32_t k = 0; k < NSQ; ++k)
-        if (lane + 64 * k < NSG) s_sc[mw][lane + 64 * k] = scg[k];
-    __builtin_amdgcn_wave_barrier();
-    float sg[RW][GQ], su[RW][GQ];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (uint32_t q = 0; q < GQ; ++q) {
-            const uint32_t b = (1024 * q + GB * lane) / CZ_BLOCK;
-            sg[r][q] = s_sc[mw][r * 2 * NBH + b];
-            su[r][q] = s_sc[mw][r * 2 * NBH + NBH + b];
-        }
-    float xv[NB];
-#pragma unroll
-    for (uint32_t q = 0; q < GQ; ++q) {
-        const float4 *xs = reinterpret_cast<const float4 *>(s_x + 1024 * q + GB * lane);
-#pragma unroll
-        for (uint32_t k = 0; k < GB / 4; ++k) {
-            const float4 t = xs[k];
-            xv[GB * q + 4 * k] = t.x; xv[GB * q + 4 * k + 1] = t.y; xv[GB * q + 4 * k + 2] = t.z; xv[GB * q + 4 * k + 3] = t.w;
-        }
-    }
     // gated product of row r: h = g_z * silu(Wg x) * (Wu x), to its place in block r
+    auto gated_products = [&]() __attribute__((always_inline)) {
+        float gz[RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        float ag = 0.0f, au = 0.0f;
+        for (int r = 0; r < RW; ++r) gz[r] = s_gate[s_fp[zr[r]]];
+        // ---- the scales to the lanes that use them
+#pragma unroll
+        for (uint32_t k = 0; k < NSQ; ++k)
+            if (lane + 64 * k < NSG) s_sc[mw][lane + 64 * k] = scg[k];
+        __builtin_amdgcn_wave_barrier();
+        float sg[RW][GQ], su[RW][GQ];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (uint32_t q = 0; q < GQ; ++q) {
+                const uint32_t b = (1024 * q + GB * lane) / CZ_BLOCK;
+                sg[r][q] = s_sc[mw][r * 2 * NBH + b];
+                su[r][q] = s_sc[mw][r * 2 * NBH + NBH + b];
+            }
+        float xv[NB];
 #pragma unroll
         for (uint32_t q = 0; q < GQ; ++q) {
-            float pg = 0.0f, pu = 0.0f;
+            const float4 *xs = reinterpret_cast<const float4 *>(s_x + 1024 * q + GB * lane);
 #pragma unroll
             for (uint32_t k = 0; k < GB / 4; ++k) {
-                pg = cz_dot4_raw(dg[r][GB / 4 * q + k], &xv[GB * q + 4 * k], pg);
-                pu = cz_dot4_raw(du[r][GB / 4 * q + k], &xv[GB * q + 4 * k], pu);
+                const float4 t = xs[k];
+                xv[GB * q + 4 * k] = t.x; xv[GB * q + 4 * k + 1] = t.y; xv[GB * q + 4 * k + 2] = t.z; xv[GB * q + 4 * k + 3] = t.w;
             }
-            ag = __builtin_fmaf(pg, sg[r][q], ag);
-            au = __builtin_fmaf(pu, su[r][q], au);
         }
-        ag = cz_wave_sum_dpp(ag);
-        au = cz_wave_sum_dpp(au);
-        if (lane == (uint32_t)r)
-            A.hx[(uint64_t)xcd * CR + CZ_BLOCK * r + rib] = cz_tagged(tag, gz[r] * (cz_silu_fast(ag) * au));
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            float ag = 0.0f, au = 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < GQ; ++q) {
+                float pg = 0.0f, pu = 0.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < GB / 4; ++k) {
+                    pg = cz_dot4_raw(dg[r][GB / 4 * q + k], &xv[GB * q + 4 * k], pg);
+                    pu = cz_dot4_raw(du[r][GB / 4 * q + k], &xv[GB * q + 4 * k], pu);
+                }
+                ag = __builtin_fmaf(pg, sg[r][q], ag);
+                au = __builtin_fmaf(pu, su[r][q], au);
+            }
+            ag = cz_wave_sum_dpp(ag);
+            au = cz_wave_sum_dpp(au);
+            if (lane == (uint32_t)r)
+                A.hx[(uint64_t)xcd * CR + CZ_BLOCK * r + rib] = cz_tagged(tag, gz[r] * (cz_silu_fast(ag) * au));
+        }
+    };
+    {
+        const uint32_t rl = s_rl;
+        bool any = false;  // uniform: a row of the wave loads after the routing
+#pragma unroll
+        for (int r = 0; r < RW; ++r) any = any || ((rl >> zr[r]) & 1u) != 0u;
+        if (!any) {
+            // every row was requested before the routing, in the order the
+            // products use them: the waits before row r's products cover its
+            // own rows only, not the down rows requested after them (a join
+            // with the path below would make them wait for nearly every
+            // request in flight); the markers keep the two copies apart
+            gated_products();
+            asm volatile("; gated products: every row requested before the routing");
+        } else {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                if ((rl >> zr[r]) & 1u) slr[r] = cz_slot(L, min(s_idx[s_fp[zr[r]]], E - 1));
+            load_scales();
+            load_down_scale();
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                if ((rl >> zr[r]) & 1u) load_row(r);
+#pragma unroll
+            for (int i = 0; i < RW; ++i)
+                if ((rl >> zr[i]) & 1u) load_down(i);
+            gated_products();
+            asm volatile("; gated products: rows requested after the routing");
+        }
     }
 
     // ---- dequantised down weights (e4m3 * block scale, fp8.zig:105), while
