@@ -758,7 +758,7 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
     const uint32_t mts = (uint32_t)(S + CZ_GG_M - 1) / CZ_GG_M;
     const uint64_t sk = (uint64_t)S * L.K;
     auto quant3 = [&](const float *src, uint64_t rows, uint32_t K, uint8_t *q, uint8_t *e) {
-        const uint64_t n = rows * (K / 32);
+        const uint64_t n = rows * K / 4;  // one float4 per thread
         k_quant3<<<(uint32_t)((n + 255) / 256), 256, 0, st>>>(src, (uint32_t)rows, K, q, rows * K, e, rows * K / 32);
     };
     if (f8 && !xq_rms) quant3(G.xn, (uint64_t)S, L.H, w.xq, w.xe);  // no RMS rows kernel splits x

@@ -630,41 +630,32 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem PR, GGProb
 // second; the exponent of row m, group b comes from lane m + 32 b.
 // ---------------------------------------------------------------------------
 
-// E4M3 of v (|v| <= 448), round to nearest even; byte in the low 8 bits.
-// Rows of K columns (K % 32 == 0) to three E4M3 terms (cz_q3_scale): one
-// thread per 32 columns of a row.  For inputs no producing kernel splits.
+// Rows of K columns (K % 32 == 0) to three E4M3 terms (cz_q3_scale): each
+// 32-column group is 8 consecutive lanes with one float4 each, so a wave's
+// loads and term stores are contiguous; the group's |max| goes round its 8
+// lanes by DPP.  For inputs no producing kernel splits.
 __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, uint32_t rows, uint32_t K,
                                                uint8_t *__restrict__ q, uint64_t q_plane, uint8_t *__restrict__ e,
                                                uint64_t e_plane) {
-    const uint32_t ng = K / 32;
-    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (uint64_t)rows * ng) return;
-    const uint64_t row = gid / ng, grp = gid - row * ng;
-    const float4 *p = reinterpret_cast<const float4 *>(src + row * K + grp * 32);
-    float r[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 v = p[i];
-        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
-    }
+    const uint64_t g4 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
+    // whole 8-lane groups leave together (rows * K / 4 is a multiple of 8)
+    if (g4 >= (uint64_t)rows * K / 4) return;
+    const float4 v = reinterpret_cast<const float4 *>(src)[g4];
+    float r[4] = {v.x, v.y, v.z, v.w};
+    const uint64_t el = 4 * g4;  // first element: row el / K, column el % K
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        float amax = 0.0f;
+        float am = fmaxf(fmaxf(__builtin_fabsf(r[0]), __builtin_fabsf(r[1])),
+                         fmaxf(__builtin_fabsf(r[2]), __builtin_fabsf(r[3])));
+        am = fmaxf(am, cz_dpp<0xB1>(am));   // lanes xor 1
+        am = fmaxf(am, cz_dpp<0x4E>(am));   // xor 2
+        am = fmaxf(am, cz_dpp<0x141>(am));  // the mirror within 8: every lane of the 8
+        const CzQ3 sc = cz_q3_scale(am);
+        uint32_t word = 0;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, __builtin_fabsf(r[i]));
-        const CzQ3 sc = cz_q3_scale(amax);
-        uint32_t w[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[4 * i + j], sc) << (8 * j);
-            w[i] = word;
-        }
-        uint4 *qo = reinterpret_cast<uint4 *>(q + t * q_plane + row * K + grp * 32);
-        qo[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        qo[1] = make_uint4(w[4], w[5], w[6], w[7]);
-        e[t * e_plane + row * ng + grp] = (uint8_t)sc.eb;
+        for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[j], sc) << (8 * j);
+        *reinterpret_cast<uint32_t *>(q + t * q_plane + el) = word;
+        if ((g4 & 7u) == 0) e[t * e_plane + el / 32] = (uint8_t)sc.eb;
     }
 }
 
