@@ -463,6 +463,49 @@ def stream_bench(args) -> None:
     log(f"stream: {steps} steps, {wall * 1e3 / steps:.2f} ms/token, {tok_s:.1f} tok/s; hit rate {hit:.3f}; "
         f"H2D {st['bytes_h2d'] / 1e9:.2f} GB ({h2d_gbs:.1f} GB/s; link {link_gbs:.1f} GB/s); {st}; "
         f"untimed drift bookkeeping {harness * 1e3 / steps:.2f} ms/step")
+    # parity at the full size (after the timed region): a streamed layer runs
+    # the resident three-kernel decode's kernels on the same bytes, so the 48
+    # layers made resident again from the streamed layers' own bytes (router
+    # read back, experts from the host slabs, the same current router
+    # biases) must give the streamed chain's bits token after token
+    parity = None
+    if args.parity_layers > 0:
+        prev_fd = hip.colizig_hip_set_fused_decode(0)
+        try:
+            t1 = time.time()
+            w_slot, P = 3 * mat, moe.packed_expert_bytes(d)
+            for l in range(NL):
+                Lr = moe.Layer.load(NL + l, d, moe.Layer(l, d, True).read_router())
+                if args.split_slabs:
+                    wa = host[l][0].view(np.uint8).reshape(E, w_slot)
+                    sa = host[l][1].view(np.float32).reshape(E, 3 * nsc)
+                else:
+                    a = host[l][0].view(np.uint8).reshape(E, P)
+                    wa, sa = a[:, :w_slot], a[:, w_slot:].view(np.float32)
+                for e in range(E):
+                    w, sc = wa[e], sa[e]
+                    Lr.load_expert(e, w[:mat].reshape(I, H), sc[:nsc].reshape(nblk(I), nblk(H)),
+                                   w[mat:2 * mat].reshape(I, H), sc[nsc:2 * nsc].reshape(nblk(I), nblk(H)),
+                                   w[2 * mat:].reshape(H, I), sc[2 * nsc:].reshape(nblk(H), nblk(I)))
+                lp = -1.2 * np.log(ranks[l].astype(np.float64) + 1.0)
+                Lr.set_router_bias((lp - lp.mean()).astype(np.float32))
+            log(f"parity: {NL} resident copies of the streamed layers in {time.time() - t1:.1f}s")
+            xr = moe.DeviceBuffer(x0.nbytes)
+            xr.upload(xb.download(np.empty_like(x0)))
+            ntok, same = 8, True
+            for _ in range(ntok):
+                if hip.colizig_hip_stream_decode(0, NL, xb.ptr, 1, eps) != 0 or \
+                        hip.colizig_hip_chain_decode(NL, NL, xr.ptr, 1, eps, None, None, None, None) != 0:
+                    raise RuntimeError(f"parity pass failed: {_lib.last_error()}")
+                assert hip.colizig_hip_sync() == 0
+                a, b = xb.download(np.empty_like(x0)), xr.download(np.empty_like(x0))
+                same = same and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+            parity = {"reference": f"the same {NL} layers resident (three-kernel decode) from the same x",
+                      "tokens": ntok, "bit_identical": same}
+            xr.free()
+        finally:
+            hip.colizig_hip_set_fused_decode(prev_fd)
+        log(f"parity: {parity}")
     line = {
         "metric": "MoE decode tok/s, expert-streaming tier (16 GB HBM pool, 29 GB pinned host), Qwen3-30B-A3B "
                   "shape, 1 MI355X",
@@ -477,6 +520,7 @@ def stream_bench(args) -> None:
         "token_level_prediction_accuracy": round(st["tok_correct"] / max(st["tok_predicted"], 1), 4),
         "roofline": {"bound": "h2d", "achieved": round(h2d_gbs, 2), "peak": round(link_gbs, 2), "unit": "GB/s",
                      "frac": round(h2d_gbs / link_gbs, 3), "traffic": None, "scope": "host->HBM fills"},
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
     # the pinned slabs in `host` stay allocated until the process ends (the layers point at them)
