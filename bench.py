@@ -327,6 +327,29 @@ def prefill_bench(args) -> None:
     log(f"prefill: {S} tokens x {NL} layers in {ms:.3f} ms ({tok_s:.0f} tok/s); experts touched per layer "
         f"{min(touched)}..{max(touched)}, hottest expert {max(hottest)} of {S} tokens; {gbs:.0f} GB/s; "
         f"{step_flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
+    # token independence at the full size (after the timed region): the MoE
+    # treats tokens independently (per-row activation terms, per-row GEMM
+    # sums, each token's combine in its pick order), so the first 64 tokens
+    # through the 48 layers on their own (still the grouped regime) must get
+    # the bits they got inside the whole step
+    parity = None
+    if args.parity_layers > 0 and S > 64:
+        P = 64
+        xa, xp = moe.DeviceBuffer(x0.nbytes), moe.DeviceBuffer(P * H * 4)
+        xa.upload(x0)
+        xp.upload(np.ascontiguousarray(x0[:P]))
+        if hip.colizig_hip_chain_decode(0, NL, xa.ptr, S, eps, None, None, None, None) != 0 or \
+                hip.colizig_hip_chain_decode(0, NL, xp.ptr, P, eps, None, None, None, None) != 0:
+            raise RuntimeError(f"parity pass failed: {_lib.last_error()}")
+        assert hip.colizig_hip_sync() == 0
+        a = xa.download(np.empty_like(x0))[:P]
+        b = xp.download(np.empty((P, H), np.float32))
+        parity = {"property": f"the first {P} tokens through the {NL} layers alone vs inside the {S}-token step",
+                  "bit_identical": bool(np.array_equal(a.view(np.uint32), b.view(np.uint32))),
+                  "max_abs_diff": float(np.max(np.abs(a - b)))}
+        xa.free()
+        xp.free()
+        log(f"parity: {parity}")
     line = {
         "metric": "MoE prefill tok/s (512-token step, Zipf(1.1) routing), Qwen3-30B-A3B shape, 1 MI355X",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -343,6 +366,7 @@ def prefill_bench(args) -> None:
         "mfma_peak_tflops": 5000.0 if fp8 else 2500.0,
         "mfma_frac": round(step_flops / (ms * 1e-3) / 1e12 / (5000.0 if fp8 else 2500.0), 4),
         "experts_touched_per_layer": [min(touched), max(touched)],
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
 
