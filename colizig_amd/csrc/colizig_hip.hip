@@ -783,7 +783,10 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         P.ae = w.xe;
         P.aq_plane = (uint64_t)S * L.H;
         P.ae_plane = (uint64_t)S * L.H / 32;
-        P.c = w.h;
+        P.cq = w.hq;  // the gate/up GEMM writes h as the down GEMM's three terms
+        P.ce = w.he;
+        P.cq_plane = sk * L.I;
+        P.ce_plane = sk * L.I / 32;
     }
     constexpr uint32_t cu = cz_gg_cols<GG_GATEUP>(), cd = cz_gg_cols<GG_DOWN>();
     // the shared expert's items run in the same launches as the routed ones
@@ -799,7 +802,10 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         Q.N = L.SI;
         Q.c_hi = w.hsh;
         Q.c_lo = w.hsl;
-        Q.c = w.hs;
+        Q.cq = w.hsq;
+        Q.ce = w.hse;
+        Q.cq_plane = (uint64_t)S * L.SI;
+        Q.ce_plane = (uint64_t)S * L.SI / 32;
         Q.routed = 0;
         Q.rows_total = (uint32_t)S;
     }
@@ -808,10 +814,6 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         k_gg8<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
     else
         k_gg<GG_GATEUP><<<qu + gg_blocks(G.max_tiles, L.I, cu), 256, 0, st>>>(G, P, Q);
-    if (f8) {
-        quant3(w.h, sk, L.I, w.hq, w.he);
-        if (L.SI) quant3(w.hs, (uint64_t)S, L.SI, w.hsq, w.hse);
-    }
 
     // down
     GGProblem D{};

@@ -334,10 +334,14 @@ struct GGProblem {
     int routed;             // 1: tiles from the dispatch table; 0: shared (rows = tokens in order)
     uint32_t rows_total;    // shared: S
     // FP8-MFMA form (k_gg8): A rows as three E4M3 terms with E8M0 exponents
-    // per 32 columns (cz_q3_scale); GATEUP writes h as f32 rows to c
+    // per 32 columns (cz_q3_scale); GATEUP writes h in the same form, the
+    // A rows of the down GEMM
     const uint8_t *aq;      // [3][rows][Kd] (term planes aq_plane bytes apart)
     const uint8_t *ae;      // [3][rows][Kd/32] (planes ae_plane bytes apart)
     uint64_t aq_plane, ae_plane;
+    uint8_t *cq;            // GATEUP: h as [3][rows][N] terms (planes cq_plane bytes apart)
+    uint8_t *ce;            // GATEUP: its exponents [3][rows][N/32] (planes ce_plane bytes apart)
+    uint64_t cq_plane, ce_plane;
 };
 
 // Output columns of one workgroup: 4 waves x 2 subtiles of 32 columns.  A
@@ -630,10 +634,10 @@ __global__ __launch_bounds__(256, 3) void k_gg(GroupArgs G, GGProblem PR, GGProb
 // second; the exponent of row m, group b comes from lane m + 32 b.
 // ---------------------------------------------------------------------------
 
-// Rows of K columns (K % 32 == 0) to three E4M3 terms (cz_q3_scale): each
+// Rows of K columns (K % 32 == 0) to three E4M3 terms (cz_q3_group4): each
 // 32-column group is 8 consecutive lanes with one float4 each, so a wave's
-// loads and term stores are contiguous; the group's |max| goes round its 8
-// lanes by DPP.  For inputs no producing kernel splits.
+// loads and term stores are contiguous.  For inputs no producing kernel
+// splits (x without the RMS rows kernel).
 __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, uint32_t rows, uint32_t K,
                                                uint8_t *__restrict__ q, uint64_t q_plane, uint8_t *__restrict__ e,
                                                uint64_t e_plane) {
@@ -643,20 +647,7 @@ __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, u
     const float4 v = reinterpret_cast<const float4 *>(src)[g4];
     float r[4] = {v.x, v.y, v.z, v.w};
     const uint64_t el = 4 * g4;  // first element: row el / K, column el % K
-#pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        float am = fmaxf(fmaxf(__builtin_fabsf(r[0]), __builtin_fabsf(r[1])),
-                         fmaxf(__builtin_fabsf(r[2]), __builtin_fabsf(r[3])));
-        am = fmaxf(am, cz_dpp<0xB1>(am));   // lanes xor 1
-        am = fmaxf(am, cz_dpp<0x4E>(am));   // xor 2
-        am = fmaxf(am, cz_dpp<0x141>(am));  // the mirror within 8: every lane of the 8
-        const CzQ3 sc = cz_q3_scale(am);
-        uint32_t word = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[j], sc) << (8 * j);
-        *reinterpret_cast<uint32_t *>(q + t * q_plane + el) = word;
-        if ((g4 & 7u) == 0) e[t * e_plane + el / 32] = (uint8_t)sc.eb;
-    }
+    cz_q3_group4(r, q + el, q_plane, e + el / 32, e_plane, (g4 & 7u) == 0, true);
 }
 
 typedef int cz_i8x32 __attribute__((ext_vector_type(8)));
@@ -666,6 +657,7 @@ typedef int cz_i8x32 __attribute__((ext_vector_type(8)));
 // exponents: 3 planes x CZ_GG_M rows x 4 bytes.
 #define CZ_GG8_APLANE (CZ_GG_M * 128)
 #define CZ_GG8_EOFF (3 * CZ_GG8_APLANE)
+#define CZ_GG8_HT 36  // floats per row of a wave's h tile in its weight stage (144 B: float4-aligned)
 __device__ __forceinline__ uint32_t cz_gg8_off(uint32_t r, uint32_t c) { return r * 128u + ((c ^ (r & 7u)) << 4); }
 
 template <int MODE>
@@ -836,14 +828,36 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
     }
 #undef CZ_GG8_LOAD
 #undef CZ_GG8_STORE
+    if constexpr (MODE == GG_GATEUP) {
+        // h = silu(g) * u of the wave's 32 rows x 32 columns (one 32-column
+        // group) goes through the wave's own weight stage (its DS operations
+        // stay in program order, so no barrier) to k_quant3's layout, 8 lanes
+        // per row with four columns each, and leaves as the three E4M3 terms
+        // of the down GEMM's A rows: the bytes k_quant3 makes of the f32 rows
+        float *ht = reinterpret_cast<float *>(lw);  // [32][CZ_GG8_HT], 4.5 KB of the 9 KB stage
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
-        const uint32_t dst = s_rowdst[r];
-        if (dst == ~0u) continue;
-        if constexpr (MODE == GG_GATEUP) {
-            P.c[(uint64_t)dst * P.N + ncol[0]] = cz_silu_fast(acc[0][i] * cur[0]) * (acc[1][i] * cur[1]);
-        } else {
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
+            ht[r * CZ_GG8_HT + (lane & 31u)] = cz_silu_fast(acc[0][i] * cur[0]) * (acc[1][i] * cur[1]);
+        }
+        const uint32_t nb = ncol[0] - (lane & 31u), c4 = lane & 7u;  // nb: the wave's first column
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            // rows of padding (dst ~0u) hold a copy of the tile's last row:
+            // finite, quantised with the rest, not stored
+            const uint32_t r = 8u * p + (lane >> 3);
+            const float4 v = *reinterpret_cast<const float4 *>(ht + r * CZ_GG8_HT + 4u * c4);
+            float rv[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t dst = s_rowdst[r];
+            const uint64_t o = (uint64_t)(dst == ~0u ? 0u : dst) * P.N + nb;
+            cz_q3_group4(rv, P.cq + o + 4u * c4, P.cq_plane, P.ce + o / 32u, P.ce_plane, c4 == 0, dst != ~0u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
+            const uint32_t dst = s_rowdst[r];
+            if (dst == ~0u) continue;
 #pragma unroll
             for (int m = 0; m < 2; ++m) P.c[(uint64_t)dst * P.N + ncol[m]] = acc[m][i] * cur[m];
         }

@@ -461,6 +461,32 @@ __device__ __forceinline__ uint32_t cz_q3_term(float &r, const CzQ3 &s) {
     return b;
 }
 
+// Four consecutive columns r[0..3] of a 32-column group spread over 8
+// consecutive lanes (lane % 8 = column / 4 within the group) to three E4M3
+// terms: the group's |max| goes round its 8 lanes by DPP, the lane's four
+// bytes of term t go to q + t * q_plane (a 4-byte aligned word), and the
+// group's exponent byte of term t to e + t * e_plane from the lead lane.  All
+// 8 lanes of a group execute it together; store = false skips the stores only.
+__device__ __forceinline__ void cz_q3_group4(float (&r)[4], uint8_t *q, uint64_t q_plane, uint8_t *e,
+                                             uint64_t e_plane, bool lead, bool store) {
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        float am = fmaxf(fmaxf(__builtin_fabsf(r[0]), __builtin_fabsf(r[1])),
+                         fmaxf(__builtin_fabsf(r[2]), __builtin_fabsf(r[3])));
+        am = fmaxf(am, cz_dpp<0xB1>(am));   // lanes xor 1
+        am = fmaxf(am, cz_dpp<0x4E>(am));   // xor 2
+        am = fmaxf(am, cz_dpp<0x141>(am));  // the mirror within 8: every lane of the 8
+        const CzQ3 sc = cz_q3_scale(am);
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[j], sc) << (8 * j);
+        if (store) {
+            *reinterpret_cast<uint32_t *>(q + t * q_plane) = word;
+            if (lead) e[t * e_plane] = (uint8_t)sc.eb;
+        }
+    }
+}
+
 // One workgroup of 256 threads per token row (H % 256 == 0, H <= 1024 Q):
 // the row is requested at once as 128-bit loads (Q per thread) and staged in
 // LDS; wave 0 forms the f64 sum of squares (cz_rms_inv), every thread then
@@ -530,21 +556,8 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
         }
         if (A.xq) {  // the group of 32 columns is 8 consecutive lanes (H % 32 == 0: whole groups active)
             float r[4] = {y.x, y.y, y.z, y.w};
-            const uint64_t qp = (uint64_t)A.S * H, ep = (uint64_t)A.S * (H / 32);
-#pragma unroll
-            for (int t = 0; t < 3; ++t) {
-                float am = fmaxf(fmaxf(__builtin_fabsf(r[0]), __builtin_fabsf(r[1])),
-                                 fmaxf(__builtin_fabsf(r[2]), __builtin_fabsf(r[3])));
-                am = fmaxf(am, cz_dpp<0xB1>(am));   // lanes xor 1
-                am = fmaxf(am, cz_dpp<0x4E>(am));   // xor 2
-                am = fmaxf(am, cz_dpp<0x141>(am));  // the mirror within 8: every lane of the 8
-                const CzQ3 sc = cz_q3_scale(am);
-                uint32_t word = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) word |= cz_q3_term(r[j], sc) << (8 * j);
-                reinterpret_cast<uint32_t *>(A.xq + t * qp + row)[q] = word;
-                if ((q & 7u) == 0) A.xe[t * ep + (uint64_t)blockIdx.x * (H / 32) + q / 8] = (uint8_t)sc.eb;
-            }
+            cz_q3_group4(r, A.xq + row + 4 * q, (uint64_t)A.S * H, A.xe + (uint64_t)blockIdx.x * (H / 32) + q / 8,
+                         (uint64_t)A.S * (H / 32), (q & 7u) == 0, true);
         }
     }
 }
