@@ -38,9 +38,9 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # HBM bytes per launch of the one-launch layer kernel on this workload,
 # measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by
 # what the same counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0,
-# WRITE_SIZE x 1.0): 24442.2 KiB fetched, 129.1 KiB written per dispatch
+# WRITE_SIZE x 1.0): 24431.5 KiB fetched, 134.5 KiB written per dispatch
 # (the mean over a step's 47 launches with predicted experts and its first).
-LAYER_TRAFFIC_BYTES = int(round((24442.2 * 2.0 + 129.1) * 1024))
+LAYER_TRAFFIC_BYTES = int(round((24431.5 * 2.0 + 134.5) * 1024))
 
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
