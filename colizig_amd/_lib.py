@@ -97,6 +97,8 @@ SIGNATURES = {
     "colizig_hip_set_fused_decode": (ctypes.c_int, [ctypes.c_int]),
     "colizig_hip_set_fused_predict": (ctypes.c_int, [ctypes.c_int]),
     "colizig_hip_fused_predict_stats": (ctypes.c_int, [ctypes.c_void_p]),
+    "colizig_hip_fused_placement": (ctypes.c_int, []),
+    "colizig_hip_set_fused_fault": (ctypes.c_int, [ctypes.c_int]),
     "colizig_hip_fused_decode_active": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]),
     "colizig_hip_chain_fused_times": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_float,
                                                      ctypes.c_int, vp]),
@@ -110,6 +112,7 @@ SIGNATURES = {
     "colizig_hip_stream_stats": (ctypes.c_int, [c_u64p, ctypes.c_int]),
     "colizig_hip_stream_pool_free": (ctypes.c_int, []),
     "colizig_hip_set_prefill_fp8": (ctypes.c_int, [ctypes.c_int]),
+    "colizig_hip_work_bytes": (ctypes.c_int, [c_u64p]),
     "colizig_hip_layer_set_router_bf16": (ctypes.c_int, [ctypes.c_uint32, vp]),
     "colizig_hip_layer_set_shared_native": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_int, vp, vp, vp, vp]),
     "colizig_hip_plan_hbm": (ctypes.c_int, [ctypes.POINTER(Dims), ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,

@@ -220,6 +220,8 @@ struct FusedState {
     uint32_t *err_host = nullptr;    // host-coherent error word
     uint32_t *err_dev = nullptr;     // its device address
     size_t cap_h = 0, cap_e = 0, cap_ki = 0;
+    bool placement_ok = false;       // the init census found the workgroup placement the kernel needs
+    int fault_pos = -1;              // test hook: the chain position whose polls never match
 };
 
 struct Ctx {
@@ -342,10 +344,13 @@ int ensure_work_grouped(const colizig_dims &d, int S) {
         grow(&w.tok_order, &w.cap_tok_order, sk) || grow(&w.tile_expert, &w.cap_tiles, mt) ||
         grow(&w.tile_row0, &w.cap_tiles2, mt) || grow(&w.ntiles, &w.cap_ntiles, (size_t)1) ||
         grow(&w.o, &w.cap_o, sk * d.hidden) || grow(&w.os, &w.cap_os, std::max<size_t>(1, s * d.hidden)) ||
-        grow(&w.xh, &w.cap_xh, s * d.hidden) || grow(&w.xl, &w.cap_xl, s * d.hidden) ||
-        grow(&w.hh, &w.cap_hh, sk * d.inter) || grow(&w.hl, &w.cap_hl, sk * d.inter) ||
-        grow(&w.hsh, &w.cap_hsh, std::max<size_t>(1, s * d.shared_inter)) ||
-        grow(&w.hsl, &w.cap_hsl, std::max<size_t>(1, s * d.shared_inter)) ||
+        // the GEMM operands of the active mode only: f16 hi + lo splits, or
+        // three E4M3 terms and their exponents
+        (!g.prefill_fp8 &&
+         (grow(&w.xh, &w.cap_xh, s * d.hidden) || grow(&w.xl, &w.cap_xl, s * d.hidden) ||
+          grow(&w.hh, &w.cap_hh, sk * d.inter) || grow(&w.hl, &w.cap_hl, sk * d.inter) ||
+          grow(&w.hsh, &w.cap_hsh, std::max<size_t>(1, s * d.shared_inter)) ||
+          grow(&w.hsl, &w.cap_hsl, std::max<size_t>(1, s * d.shared_inter)))) ||
         (g.prefill_fp8 &&
          (grow(&w.xq, &w.cap_xq, 3 * s * d.hidden) || grow(&w.xe, &w.cap_xe, 3 * s * d.hidden / 32) ||
           grow(&w.hq, &w.cap_hq, 3 * sk * d.inter) || grow(&w.he, &w.cap_he, 3 * sk * d.inter / 32) ||
@@ -875,7 +880,7 @@ LayerHost *find_layer(uint32_t layer);
 // E <= 128, K <= 32, I a multiple of 128 and K*I/1024 in {1, 2, 4, 6, 8}.
 bool fused_ok(const LayerHost &L, int S) {
     const colizig_dims &d = L.d;
-    if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG) return false;
+    if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG || !g.fused.placement_ok) return false;
     if (d.shared_inter != 0 || d.experts > 128 || d.topk > 32 || d.inter % CZ_BLOCK || L.router_bf16)
         return false;
     if (d.hidden != 512 && d.hidden != 1024 && d.hidden != 2048) return false;
@@ -991,6 +996,7 @@ int chain_enqueue_fused(uint32_t layer0, uint32_t n, float *x_dev, float eps, fl
         A.lgpx = F.lgpx;
         A.pred_mode = F.predict >= 2 ? (uint32_t)(F.predict - 1) : 0u;
         A.pstat = F.pstat;
+        A.poll_mask = (int)p == F.fault_pos ? ~1023u : ~0u;
         const uint32_t rw = (uint32_t)((uint64_t)L.d.topk * L.d.inter / 1024);
         switch (H) {
             case 512: launch_fused_nb<8>(A, rw, st); break;
@@ -1087,6 +1093,34 @@ int fused_check_error() {
 
 uint8_t *noalloc_scratch();
 
+// The one-launch decode's placement census (k_xcd_census): true when each of
+// the 8 XCDs received exactly one workgroup of each rank 0 .. 31 of a
+// CZ_FWG-wide launch, the layout k_layer_fused's exchanges assume.  Anything
+// else (another XCD count, another dispatch order, a failed launch) keeps
+// the layers on the three-kernel path.
+bool fused_placement_census() {
+    uint32_t *d = nullptr;
+    uint32_t h[CZ_FWG];
+    bool ok = hipMalloc(&d, sizeof h) == hipSuccess;
+    if (ok) {
+        k_xcd_census<<<CZ_FWG, 64, 0, g.stream>>>(d);
+        ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(g.stream) == hipSuccess &&
+             hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess;
+    }
+    if (d) (void)hipFree(d);
+    if (!ok) return false;
+    uint32_t seen[CZ_NXCD] = {0};  // bit w: rank w seen on that XCD
+    for (uint32_t b = 0; b < CZ_FWG; ++b) {
+        if (h[b] >= CZ_NXCD) return false;
+        const uint32_t bit = 1u << (b / CZ_NXCD);
+        if (seen[h[b]] & bit) return false;
+        seen[h[b]] |= bit;
+    }
+    for (uint32_t x = 0; x < CZ_NXCD; ++x)
+        if (seen[x] != 0xffffffffu) return false;
+    return true;
+}
+
 uint64_t mix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ull;
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
@@ -1120,6 +1154,7 @@ extern "C" int colizig_cuda_init(void) {
              (size_t)(prop.totalGlobalMem >> 20));
     g.fused.cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) return -4;
+    g.fused.placement_ok = g.fused.cus == CZ_FWG && fused_placement_census();
     // the no-alloc forward's scratch address on this device; a failure is
     // reported by that entry point, which tries again
     if (!noalloc_scratch()) g_err[0] = 0;
@@ -3254,12 +3289,22 @@ namespace {
 constexpr uint32_t kCapLadder[] = {128, 96, 64, 48, 32, 24, 16, 12, 8, 6, 4};
 
 // The forward's scratch for S tokens: ensure_work + ensure_work_grouped.
+// The forward's scratch (Work) for S tokens, byte for byte what ensure_work
+// and, in the grouped regime, ensure_work_grouped allocate in the active
+// prefill mode (colizig_hip_work_bytes reports the allocation to compare).
 uint64_t work_bytes(const colizig_dims &d, uint64_t S) {
-    const uint64_t sk = S * d.topk, H = d.hidden, mt = sk / CZ_GG_M + std::min<uint64_t>(d.experts, sk) + 1;
-    const uint64_t si = std::max<uint64_t>(1, S * d.shared_inter);
+    const uint64_t sk = S * d.topk, H = d.hidden, SI = d.shared_inter;
+    const uint64_t mt = sk / CZ_GG_M + std::min<uint64_t>(d.experts, sk) + 1;
+    const uint64_t si = std::max<uint64_t>(1, S * SI);
     uint64_t b = 4 * (3 * S * H + S * d.experts + 2 * sk + S + sk * d.inter + si);  // xin, out, xn, logits, ..
+    if (SI) b += 4 * (2 * S * SI + S * H + S);  // the shared expert's gate, up, down rows and gate
+    if (S < (uint64_t)kGroupedMinTokens) return b;
     b += 4 * (2 * (uint64_t)d.experts + 1 + 3 * sk + 2 * mt + 1 + sk * H + std::max<uint64_t>(1, S * H));
-    b += 2 * (2 * S * H + 2 * sk * d.inter + 2 * si);  // f16 splits
+    if (g.prefill_fp8)  // three E4M3 terms and their exponents
+        b += 3 * (S * H + sk * d.inter) + 3 * (S * H + sk * d.inter) / 32 +
+             std::max<uint64_t>(1, 3 * S * SI) + std::max<uint64_t>(1, 3 * S * SI / 32);
+    else  // f16 hi + lo splits
+        b += 2 * (2 * S * H + 2 * sk * d.inter + 2 * si);
     return b;
 }
 }  // namespace
@@ -3311,6 +3356,21 @@ extern "C" int colizig_hip_plan_hbm(const colizig_dims *dims, uint32_t layers, u
     }
     p.total = p.fixed_resident + p.expert_bytes;
     *out = p;
+    return 0;
+}
+
+// Bytes the forward's scratch (Work) holds now: the capacities of its
+// buffers (grow-only; buffers retired by a growth are not counted).
+extern "C" int colizig_hip_work_bytes(uint64_t *out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited || !out) return -1;
+    const Work &w = g.work;
+    *out = 4 * (w.cap_xin + w.cap_out + w.cap_xn + w.cap_logits + w.cap_idx + w.cap_gates + w.cap_sgate + w.cap_h +
+                w.cap_hs + w.cap_ng + w.cap_nu + w.cap_no + w.cap_nsg + w.cap_counts + w.cap_offsets +
+                w.cap_sorted + w.cap_slot_pos + w.cap_tok_order + w.cap_tiles + w.cap_tiles2 + w.cap_ntiles +
+                w.cap_o + w.cap_os) +
+           2 * (w.cap_xh + w.cap_xl + w.cap_hh + w.cap_hl + w.cap_hsh + w.cap_hsl) +
+           (w.cap_xq + w.cap_xe + w.cap_hq + w.cap_he + w.cap_hsq + w.cap_hse);
     return 0;
 }
 
@@ -3430,6 +3490,26 @@ extern "C" int colizig_hip_fused_predict_stats(uint64_t *out) {
     CZ_CHECK(hipMemcpy(out, g.fused.pstat, 2 * sizeof(uint64_t), hipMemcpyDeviceToHost), -5);
     CZ_CHECK(hipMemset(g.fused.pstat, 0, 2 * sizeof(uint64_t)), -5);
     return 0;
+}
+
+// Test hook: from the next chain on, the layer at chain position pos polls
+// for a tag no layer writes, so its bounded waits give up after 20 ms, the
+// kernel finishes with what it read and colizig_hip_sync reports -5 (-1:
+// off).  Returns the previous position.
+extern "C" int colizig_hip_set_fused_fault(int pos) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = g.fused.fault_pos;
+    g.fused.fault_pos = pos < 0 ? -1 : pos;
+    return prev;
+}
+
+// 1 when the init census found the workgroup placement the one-launch decode
+// needs (8 XCDs, one workgroup of each rank per XCD), 0 otherwise, -1 before
+// init.
+extern "C" int colizig_hip_fused_placement(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.inited) return -1;
+    return g.fused.placement_ok ? 1 : 0;
 }
 
 extern "C" int colizig_hip_fused_decode_active(uint32_t layer0, uint32_t nlayers, int S) {

@@ -76,6 +76,8 @@ struct FusedArgs {
     const float *rbias_next;      // nullable [E] its bias
     uint32_t pred_mode;           // test hooks: 0 as computed, 1 no slot matched, 2 slot 0 unmatched
     unsigned long long *pstat;    // [2] slots predicted, slots whose prediction was picked
+    uint32_t poll_mask;           // ~0u; test hook: ~1023u makes this layer's polls wait for a tag
+                                  // no layer writes (a written tag's low 10 bits are never 0)
 };
 
 typedef float cz_f4 __attribute__((ext_vector_type(4)));
@@ -250,6 +252,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     const uint32_t xcd = xcc & (CZ_NXCD - 1), w = blockIdx.x / CZ_NXCD;
     // the run counter through the scalar cache (written before this launch)
     const uint32_t tag = (*(const __attribute__((address_space(4))) uint32_t *)A.run << 10) | ((A.pos + 1u) & 1023u);
+    const uint32_t ptag = tag & A.poll_mask;  // the tag this layer's polls wait for
     const uint32_t e0 = w * CZ_FEPW;
     const uint32_t ne = E > e0 ? min((uint32_t)CZ_FEPW, E - e0) : 0u;
     if (tid == 0) s_stage = 0;
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         // ---- wave 0: the XCD's logits, routing (moe.zig:435-463, the
         // single-wave routing of the decode kernels: no workgroup barrier)
         float lg[2] = {0.0f, 0.0f};
-        cz_poll_tagged<2>(A.lgx + (uint64_t)xcd * E, E, tag, lg, A.err);
+        cz_poll_tagged<2>(A.lgx + (uint64_t)xcd * E, E, ptag, lg, A.err);
         uint32_t o_pos = 0, o_id = 0;
         float o_gate = 0.0f;
         cz_route_wave_regs<2>(lg, E, K, L.norm_topk, s_idx, s_gate, o_pos, o_id, o_gate);
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         // top-k of the exchanged logits)
         if (pred_out && w == 0) {
             float pl[2] = {0.0f, 0.0f};
-            cz_poll_tagged<2>(A.lgpx, E, tag, pl, A.err);
+            cz_poll_tagged<2>(A.lgpx, E, ptag, pl, A.err);
             const uint32_t pe = cz_topk_wave(pl, E, K);
             if (lane < K) A.pred_out[lane] = pe;
         }
@@ -645,7 +648,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     // its own LDS copy: no workgroup barrier), then the down rows
     {
         float hq[NQH];
-        cz_poll_tagged<NQH>(A.hx + xcd * CR, CR, tag, hq, A.err);
+        cz_poll_tagged<NQH>(A.hx + xcd * CR, CR, ptag, hq, A.err);
 #pragma unroll
         for (uint32_t q = 0; q < NQH; ++q) s_h[mw][lane + 64 * q] = hq[q];
     }
@@ -681,6 +684,16 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         acc = acc + cz_dpp<0x141>(acc);  // row_half_mirror: lane i <-> 7 - i of its 8
         if (dj == 0 && dq < DR) A.pout[(uint64_t)xcd * H + r0 + DR * p + dq] = acc;
     }
+}
+
+// Placement census for the one-launch decode: workgroup b of a CZ_FWG-wide
+// launch records the XCD it runs on.  The layer kernel needs every XCD to
+// receive exactly one workgroup of each rank b / 8 = 0 .. 31 (the round-robin
+// dispatch of workgroups over the XCDs); the host checks this once at init.
+__global__ __launch_bounds__(64) void k_xcd_census(uint32_t *xcc_of) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if (threadIdx.x == 0) xcc_of[blockIdx.x] = xcc & 0xffu;
 }
 
 // After the last layer: x = residual + (((p0 + p1) + ...) + p7); advances the

@@ -258,6 +258,21 @@ int colizig_hip_set_fused_predict(int mode);
  * -1 before any one-launch decode ran.  No counterpart in the reference. */
 int colizig_hip_fused_predict_stats(uint64_t *out);
 
+/* The one-launch decode's placement check: 1 when the census at init found
+ * each of the 8 XCDs running exactly one workgroup of each rank 0..31 of a
+ * 256-workgroup launch (the layout its exchanges inside an XCD need), 0
+ * otherwise (every chain then takes the three-kernel decode), -1 before
+ * init.  No counterpart in the reference. */
+int colizig_hip_fused_placement(void);
+
+/* Test hook of the one-launch decode's failure path: from the next chain on,
+ * the layer at chain position pos (0-based; -1 turns the hook off) polls for
+ * a tag no layer writes.  Its bounded waits give up after 20 ms, its kernel
+ * finishes with what it read, and the next colizig_hip_sync returns -5 with
+ * a message (the step's results are invalid).  Returns the previous
+ * position.  No counterpart in the reference. */
+int colizig_hip_set_fused_fault(int pos);
+
 /* The grouped regime's GEMMs (prefill, batch decode) on FP8 MFMA
  * (v_mfma_scale_f32_32x32x64_f8f6f4: E4M3 weights as they are, the A rows as
  * three E4M3 terms with E8M0 exponents per 32 columns; the default) when
@@ -417,6 +432,12 @@ typedef struct colizig_hbm_plan {
 } colizig_hbm_plan;
 int colizig_hip_plan_hbm(const colizig_dims *dims, uint32_t layers, uint64_t hbm_budget, uint32_t max_tokens,
                          colizig_hbm_plan *out);
+
+/* Bytes the forward's scratch holds now (grow-only; the plan's `scratch` for
+ * max_tokens counts what a forward of that many tokens allocates in the
+ * active prefill mode).  0, or -1 before init.  No counterpart in the
+ * reference. */
+int colizig_hip_work_bytes(uint64_t *out);
 
 /* Pinned host memory for the host expert slabs. */
 void *colizig_hip_host_alloc(uint64_t bytes);

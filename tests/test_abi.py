@@ -83,6 +83,7 @@ def test_no_device_error_paths():
     assert h.colizig_hip_matmul_fp8_dev_multi(1, ys, ks, os_, p(x), 1, 4, None) == -1
     st = np.zeros(2, np.uint64)
     assert h.colizig_hip_fused_predict_stats(p(st)) == -1
+    assert h.colizig_hip_fused_placement() == -1
 
 
 def test_host_side_switches():
@@ -104,6 +105,12 @@ def test_host_side_switches():
         assert h.colizig_hip_set_prefill_fp8(0) == 1
     finally:
         h.colizig_hip_set_prefill_fp8(p8)
+    ff = h.colizig_hip_set_fused_fault(2)
+    try:
+        assert h.colizig_hip_set_fused_fault(-7) == 2
+        assert h.colizig_hip_set_fused_fault(-1) == -1  # any negative position is "off"
+    finally:
+        h.colizig_hip_set_fused_fault(ff)
     fd = h.colizig_hip_set_fused_decode(0)
     try:
         assert h.colizig_hip_set_fused_decode(1) == 0
