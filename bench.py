@@ -350,6 +350,18 @@ def prefill_bench(args) -> None:
         xa.free()
         xp.free()
         log(f"parity: {parity}")
+    # the oracle's own chain from the same x0 over all the layers, on the
+    # first 64 tokens (tokens are independent, so their rows of the 512-token
+    # step are what the oracle's chain of those tokens alone gives), for the
+    # FP8 and the f16 GEMM operands; its timing is the line's CPU baseline
+    cpu = None
+    if args.parity_layers > 0 and S > 64:
+        biases = [synth.zipf_router_bias(E, 1.1, seed=7919 * l + 1) for l in range(NL)]
+        layers = [moe.Layer(l, d) for l in range(NL)]
+        res, cpu = prefill_oracle_parity(hip, moe, layers, biases, x0, c, eps, 64, 1 if fp8 else 0)
+        parity = {"token_independence": parity, "oracle_chain": res}
+        log(f"parity vs oracle chain: {res}")
+        log(f"cpu baseline: {cpu}")
     line = {
         "metric": "MoE prefill tok/s (512-token step, Zipf(1.1) routing), Qwen3-30B-A3B shape, 1 MI355X",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -367,8 +379,87 @@ def prefill_bench(args) -> None:
         "mfma_frac": round(step_flops / (ms * 1e-3) / 1e12 / (5000.0 if fp8 else 2500.0), 4),
         "experts_touched_per_layer": [min(touched), max(touched)],
         "parity": parity,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def prefill_oracle_parity(hip, moe, layers, biases, x0, c, eps, P, mode):
+    """The 48-layer prefill chain on the GPU (S = len(x0) tokens, in each
+    grouped-GEMM mode: the library's current one and f16) against the
+    oracle's own chain of the first P tokens from the same x0, layer by layer
+    (each layer's weights copied back, checked and dropped): routing bit-exact
+    on the GPU's own router inputs and the same picks as the oracle's chain,
+    the near-tie census of the oracle's decisions, router inputs and the
+    final residual stream within 1e-3 relative L2.  Returns the result per
+    mode and the oracle's timing as the CPU baseline (P tokens x all layers
+    on the host cores)."""
+    from oracle import oracle as orc
+    S, H = x0.shape
+    K = c["topk"]
+    NL = len(layers)
+    present = len(os.sched_getaffinity(0))
+    threads = min(present, 16)
+    orc.lib().czo_parallel_enable(threads)
+    modes = [mode, 0] if mode != 0 else [0]
+    gpu = {}
+    for m in modes:
+        hip.colizig_hip_set_prefill_fp8(m)
+        xb = moe.DeviceBuffer(x0.nbytes)
+        xn_t = moe.DeviceBuffer(NL * S * H * 4)
+        idx_t = moe.DeviceBuffer(NL * S * K * 4)
+        g_t = moe.DeviceBuffer(NL * S * K * 4)
+        xb.upload(x0)
+        if hip.colizig_hip_chain_decode(0, NL, xb.ptr, S, eps, xn_t.ptr, idx_t.ptr, g_t.ptr, None) != 0 or \
+                hip.colizig_hip_sync() != 0:
+            raise RuntimeError(f"prefill parity pass failed: {_lib_err()}")
+        gpu[m] = dict(x=xb.download(np.empty_like(x0))[:P].copy(),
+                      xn=xn_t.download(np.empty((NL, S, H), np.float32))[:, :P].copy(),
+                      idx=idx_t.download(np.empty((NL, S, K), np.uint32))[:, :P].copy(),
+                      gates=g_t.download(np.empty((NL, S, K), np.float32))[:, :P].copy())
+        for b in (xb, xn_t, idx_t, g_t):
+            b.free()
+    hip.colizig_hip_set_prefill_fp8(mode)
+    xo = np.ascontiguousarray(x0[:P]).copy()
+    acc = {m: dict(exact=True, worst_xn=0.0) for m in modes}
+    min_gap, oracle_s = 1 << 30, 0.0
+    for l, L in enumerate(layers):
+        host = host_layer(hip, L, c)
+        host["router_bias"] = biases[l]
+        O = orc.OracleLayer(host)
+        t0 = time.perf_counter()
+        xn_o, idx_o, _ = O.chain(xo, eps)
+        oracle_s += time.perf_counter() - t0
+        for t in range(P):  # route() takes one row
+            _, _, v = O.route(xn_o[t])
+            top = sorted(range(v.size), key=lambda e: (-float(v[e]), e))[:K + 1]
+            b = v[top].view(np.uint32).astype(np.int64)
+            min_gap = min(min_gap, int(np.min(b[:-1] - b[1:])))
+        for m in modes:
+            G = gpu[m]
+            a = acc[m]
+            a["worst_xn"] = max(a["worst_xn"], float(np.linalg.norm(G["xn"][l] - xn_o) / np.linalg.norm(xn_o)))
+            for t in range(P):
+                ri, rg, _ = O.route(G["xn"][l, t])
+                a["exact"] &= bool(np.array_equal(ri, G["idx"][l, t]) and
+                                   np.array_equal(rg.view(np.uint32), G["gates"][l, t].view(np.uint32)))
+            a["exact"] &= bool(np.array_equal(G["idx"][l], idx_o))
+        del O, host
+    names = {0: "f16", 1: "fp8", 2: "fp8"}
+    res = {"layers_checked": NL, "tokens_checked": P, "reference": f"oracle chain of the first {P} tokens from the same x0",
+           "tolerance": 1e-3, "near_tie_min_gap_ulps": min_gap}
+    for m in modes:
+        res[names[m]] = {"routing_bit_exact": acc[m]["exact"], "max_router_input_rel_l2": acc[m]["worst_xn"],
+                         "residual_rel_l2": float(np.linalg.norm(gpu[m]["x"] - xo) / np.linalg.norm(xo))}
+    cpu = {"value": round(P / oracle_s, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+           "sample": f"the oracle's chain (cz_oracle.c, the reference's CPU SIMD path restated) of {P} of the "
+                     f"{S} tokens through all {NL} layers, {oracle_s:.1f} s; host {cpu_model()}"}
+    return res, cpu
+
+
+def _lib_err() -> str:
+    from colizig_amd import _lib
+    return _lib.last_error()
 
 
 def stream_bench(args) -> None:

@@ -278,9 +278,10 @@ int colizig_hip_set_fused_fault(int pos);
  * three E4M3 terms with E8M0 exponents per 32 columns; the default) when
  * enable != 0, or on f16 MFMA (E4M3 weights widened exactly, A rows as f16
  * hi + lo); returns the previous setting.  Outputs stay within the 1e-3
- * relative L2 bar either way (FP8 about 5e-5, f16 about 3e-7 at the
- * Qwen3-30B-A3B prefill); the two run at the same speed; routing is
- * unaffected. */
+ * relative L2 bar either way: over a 48-layer Qwen3-30B-A3B prefill chain
+ * (512 tokens, 64 checked against the oracle's own chain) the residual
+ * stream is within 4.8e-5 (FP8) and 7.9e-7 (f16), and routing is bit-exact
+ * at every layer in both modes.  FP8 runs about 2% faster. */
 int colizig_hip_set_prefill_fp8(int enable);
 int colizig_hip_fused_decode_active(uint32_t layer0, uint32_t nlayers, int S);
 int colizig_hip_chain_fused_times(uint32_t layer0, uint32_t nlayers, float *x_dev, float eps, int reps,
