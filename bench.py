@@ -79,7 +79,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--parity-layers", type=int, default=48,
                     help="decode: layers of the parity check against the oracle's own chain (one token)")
-    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead", "dropin"],
+    ap.add_argument("--workload", choices=["decode", "prefill", "stream", "qwen4", "attn", "lmhead", "dropin",
+                                           "microbench"],
                     default="decode",
                     help="decode: the 48-layer batch-1 decode line (default); prefill: 48 layers x "
                          "512 tokens with Zipf(1.1) routing skew (grouped regime); stream: batch-1 decode "
@@ -134,6 +135,9 @@ def main():
         return
     if args.workload == "lmhead":
         lmhead_bench(args)
+        return
+    if args.workload == "microbench":
+        microbench(args)
         return
     if args.workload == "dropin":
         dropin_bench(args)
@@ -697,6 +701,34 @@ def qwen4_bench(args) -> None:
         hip.colizig_hip_graph_destroy(gh)
         xb.free()
         idx_t.free()
+    # after the timed regions: the batch-1 chain against the oracle's own
+    # chain from the same x0 over the first PL layers (each 3.3 GB layer
+    # copied back), and the oracle's per-layer time on the host cores as the
+    # CPU baseline, scaled to the 36-layer token
+    parity, cpu = None, None
+    PL = min(args.parity_layers, 4, NL)
+    if PL > 0:
+        from oracle import oracle as orc
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        orc.lib().czo_parallel_enable(threads)
+        t1 = time.time()
+        hosts = [orc.OracleLayer(host_layer(hip, moe.Layer(l, d), c)) for l in range(PL)]
+        copy_s = time.time() - t1
+        x0 = np.random.default_rng(101).normal(0.0, 1.0, size=(1, H)).astype(np.float32)
+        parity = parity_check(hip, moe, hosts, x0, c, 1e-6)
+        log(f"parity: {parity}")
+        xo = x0.copy()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < PL:
+            hosts[n % PL].chain(xo, 1e-6)
+            n += 1
+        per_layer_s = (time.perf_counter() - t0) / n
+        cpu = {"value": round(1.0 / (NL * per_layer_s), 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n} layer steps of the oracle's chain at batch 1 over the first {PL} layers "
+                         f"({per_layer_s * 1e3:.1f} ms per layer), scaled to the {NL}-layer token; host "
+                         f"{cpu_model()}; {copy_s:.1f} s to copy the {PL} layers back"}
+        log(f"cpu baseline: {cpu}")
+        del hosts
     line = {
         "metric": "MoE decode tok/s, Qwen4-Exp-style stack (36 L, E512 top-10 + shared), 1 MI355X",
         "value": out[1]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -706,6 +738,8 @@ def qwen4_bench(args) -> None:
         "batch1": out[1], "batch32": out[32],
         "roofline": {"bound": "hbm", "achieved": out[1]["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": out[1]["hbm_frac"], "traffic": None, "scope": "whole step, batch 1"},
+        "parity": parity,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -783,6 +817,86 @@ def attn_bench(args) -> None:
                    "qkv": "three launches" if args.attn_separate else "one launch (matmul_fp8_dev_multi)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole token, 192 launches"},
+    }))
+
+
+# tools/microbench.zig:198-298's FP8 expert matmul and its published single-
+# thread figure (docs/BENCHMARK.md:240, "FP8: fused decode+FMA")
+MICRO_I, MICRO_O, MICRO_ITERS = 2560, 640, 4000
+MICRO_REF_US, MICRO_REF_GFLOPS = 469.0, 7.0
+
+
+def microbench(args) -> None:
+    """The reference's kernel micro-benchmark restated (tools/microbench.zig:
+    198-298): one FP8 expert projection y[1, 640] = x[1, 2560] . W[640, 2560]^T
+    with 128x128 block scales, timed over 4000 back-to-back matmuls.  GPU: the
+    keyed device FP8 GEMV (the matrix resident, the input in HBM), between HIP
+    events on the library stream.  CPU: the oracle's matmulFp8 (fp8.zig:
+    215-257, the reference's CPU SIMD path restated in C) on one thread, the
+    reference's own setting.  Inputs as the reference draws them (x uniform in
+    [-1, 1), random weight bytes, scales uniform in [0.01, 0.06)), NaN
+    encodings excluded so that the two results can be compared."""
+    from colizig_amd import _lib, moe
+    from oracle import oracle as orc
+    name = moe.init()
+    log(f"device: {name}")
+    hip = _lib.hip()
+    I, O, iters = MICRO_I, MICRO_O, MICRO_ITERS
+    rng = np.random.default_rng(42)
+    x = (rng.random((1, I), dtype=np.float32) * 2 - 1).astype(np.float32)
+    w = rng.integers(0, 256, size=(O, I), dtype=np.uint8)
+    w[(w & 0x7f) == 0x7f] = 0x00  # no NaN encodings
+    s = (0.01 + rng.random(nblk(O) * nblk(I), dtype=np.float32) * 0.05).astype(np.float32)
+    moe.set_vram_budget(1 << 30)
+    key = moe.Fp8Matrix.expert_key(0, 1001, 0)
+    moe.matrix_load(key, w, s.reshape(nblk(O), nblk(I)))
+    xb, yb = moe.DeviceBuffer(I * 4), moe.DeviceBuffer(O * 4)
+    xb.upload(x)
+    for _ in range(max(args.warmup, 10)):
+        moe.matmul_fp8_dev(yb.ptr, xb.ptr, 1, I, O, key)
+    assert hip.colizig_hip_sync() == 0
+    ev0, ev1 = hip.colizig_hip_event_create(), hip.colizig_hip_event_create()
+    hip.colizig_hip_event_record(ev0, None)
+    for _ in range(iters):
+        moe.matmul_fp8_dev(yb.ptr, xb.ptr, 1, I, O, key)
+    hip.colizig_hip_event_record(ev1, None)
+    assert hip.colizig_hip_sync() == 0
+    gpu_us = hip.colizig_hip_event_elapsed_ms(ev0, ev1) * 1000.0 / iters
+    y_gpu = yb.download(np.empty((1, O), np.float32))
+    moe.set_vram_budget(0)
+    flop = 2.0 * O * I
+    # the oracle on one thread, as the reference's micro-benchmark runs
+    orc.lib().czo_parallel_disable()
+    y_cpu = orc.matmul_fp8(x, w, s, 1, I, O)
+    n, t0 = 0, time.perf_counter()
+    while n < iters and time.perf_counter() - t0 < 20.0:
+        orc.matmul_fp8(x, w, s, 1, I, O)
+        n += 1
+    cpu_us = (time.perf_counter() - t0) * 1e6 / n
+    err = float(np.linalg.norm(y_gpu - y_cpu) / np.linalg.norm(y_cpu))
+    log(f"microbench FP8 I={I} O={O} S=1: GPU {gpu_us:.2f} us/matmul ({flop / gpu_us / 1e3:.1f} GFLOP/s); "
+        f"oracle, 1 thread {cpu_us:.1f} us/matmul ({flop / cpu_us / 1e3:.2f} GFLOP/s, {n} matmuls); reference "
+        f"{MICRO_REF_US:.0f} us ({MICRO_REF_GFLOPS} GFLOP/s); GPU vs oracle rel L2 {err:.2e}")
+    wbytes = O * I + 4 * s.size
+    print(json.dumps({
+        "metric": "FP8 expert matmul (tools/microbench.zig: I=2560, O=640, S=1) us per matmul, 1 MI355X",
+        "value": round(gpu_us, 3), "unit": "us/matmul", "n_gpus": 1, "steps": iters, "warmup": max(args.warmup, 10),
+        "ms_per_step": round(gpu_us / 1000.0, 6), "higher_is_better": False, "scaling": "strong",
+        "vs_baseline": None, "dtype": "e4m3-weights/f32-accumulate",
+        "data": "synthetic (x uniform [-1, 1), random E4M3 bytes without NaN, scales uniform [0.01, 0.06))",
+        "config": {"workload": "microbench-fp8-expert-matmul", "I": I, "O": O, "S": 1, "matmuls": iters,
+                   "parallelism": "none (1 GPU)"},
+        "gflops": round(flop / gpu_us / 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(wbytes / (gpu_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(wbytes / (gpu_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "scope": "one launch; the 1.6 MB matrix stays in the caches between launches"},
+        "reference": {"us_per_matmul": MICRO_REF_US, "gflops": MICRO_REF_GFLOPS,
+                      "source": "docs/BENCHMARK.md:240 (FP8 fused decode+FMA, one thread)"},
+        "cpu_baseline": {"value": round(cpu_us, 2), "unit": "us/matmul", "cores": 1, "kind": "port",
+                         "gflops": round(flop / cpu_us / 1e3, 3),
+                         "sample": f"{n} matmuls of the oracle's matmulFp8 (cz_oracle.c) on one thread, host "
+                                   f"{cpu_model()}"},
+        "parity": {"reference": "the oracle's matmulFp8 on the same inputs", "rel_l2": err, "tolerance": 1e-3},
     }))
 
 
@@ -960,8 +1074,10 @@ def parity_check(hip, moe, orcs, x0, c, eps):
 
 
 def host_layer(hip, L, c):
-    """A registered layer copied to host memory, in the oracle's layout."""
+    """A registered layer copied to host memory, in the oracle's layout (its
+    shared expert too, when c has one)."""
     H, E, K, I = c["hidden"], c["experts"], c["topk"], c["inter"]
+    SI = c.get("shared_inter", 0)
     mat = I * H
     nsc = nblk(I) * nblk(H)
     ew = np.empty(E * 3 * mat, np.uint8)
@@ -976,8 +1092,8 @@ def host_layer(hip, L, c):
         experts.append(dict(gate_w=ew[e, 0].reshape(I, H), gate_s=es[e, 0].reshape(nblk(I), nblk(H)),
                             up_w=ew[e, 1].reshape(I, H), up_s=es[e, 1].reshape(nblk(I), nblk(H)),
                             down_w=ew[e, 2].reshape(H, I), down_s=es[e, 2].reshape(nblk(H), nblk(I))))
-    return dict(dims=dict(hidden=H, experts=E, topk=K, inter=I, shared_inter=0, norm_topk=1),
-                router=L.read_router(), experts=experts, shared=None, _slabs=(ew, es))
+    return dict(dims=dict(hidden=H, experts=E, topk=K, inter=I, shared_inter=SI, norm_topk=1),
+                router=L.read_router(), experts=experts, shared=L.read_shared() if SI else None, _slabs=(ew, es))
 
 
 def cpu_baseline(hosts, x0, eps, seconds, copy_s):
