@@ -133,6 +133,7 @@ SIGNATURES = {
     "colizig_hip_predictor_record": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, vp, ctypes.c_uint32]),
     "colizig_hip_predictor_predict": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, vp, ctypes.c_uint32]),
     "colizig_hip_predictor_stats": (ctypes.c_int, [ctypes.c_int64, c_u64p, c_u64p]),
+    "colizig_hip_predictor_predict_scored": (ctypes.c_int, [ctypes.c_int64, ctypes.c_uint32, vp, ctypes.c_uint32]),
     "colizig_hip_host_alloc": (vp, [ctypes.c_uint64]),
     "colizig_hip_host_free": (None, [vp]),
     "colizig_hip_expf_dev": (ctypes.c_int, [vp, vp, ctypes.c_int]),

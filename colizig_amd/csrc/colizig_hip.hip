@@ -8,6 +8,7 @@
 #include "cz_grouped.h"
 #include "cz_fused.h"
 #include "cz_sched.h"
+#include "cz_plan.h"
 #include "colizig_hip.h"
 
 #include <xmmintrin.h>
@@ -3274,6 +3275,20 @@ extern "C" int colizig_hip_predictor_predict(int64_t h, uint32_t layer, uint32_t
     return (int)n;
 }
 
+extern "C" int colizig_hip_predictor_predict_scored(int64_t h, uint32_t layer, colizig_prefetch_prediction *out,
+                                                    uint32_t max) {
+    static_assert(sizeof(colizig_prefetch_prediction) == sizeof(cz::PrefetchPrediction), "row layout");
+    std::lock_guard<std::mutex> lk(g_obj_mu);
+    const auto it = g_preds.find(h);
+    if (it == g_preds.end() || (max && !out)) return -1;
+    cz::PrefetchPrediction rows[64];
+    const size_t n = it->second.predict_scored(layer, rows, std::min<uint32_t>(max, 64));
+    for (size_t i = 0; i < n; ++i)
+        out[i] = colizig_prefetch_prediction{rows[i].layer, rows[i].expert, rows[i].confidence,
+                                             rows[i].expected_use_distance};
+    return (int)n;
+}
+
 extern "C" int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint64_t *correct) {
     std::lock_guard<std::mutex> lk(g_obj_mu);
     const auto it = g_preds.find(h);
@@ -3283,31 +3298,9 @@ extern "C" int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint6
     return 0;
 }
 
-// ---- HBM plan (budget.plan, budget.zig:184-264, for one GPU's HBM) --------
-namespace {
-// budget.zig:62 cap_ladder: candidate per-layer expert caps, largest first.
-constexpr uint32_t kCapLadder[] = {128, 96, 64, 48, 32, 24, 16, 12, 8, 6, 4};
-
-// The forward's scratch for S tokens: ensure_work + ensure_work_grouped.
-// The forward's scratch (Work) for S tokens, byte for byte what ensure_work
-// and, in the grouped regime, ensure_work_grouped allocate in the active
-// prefill mode (colizig_hip_work_bytes reports the allocation to compare).
-uint64_t work_bytes(const colizig_dims &d, uint64_t S) {
-    const uint64_t sk = S * d.topk, H = d.hidden, SI = d.shared_inter;
-    const uint64_t mt = sk / CZ_GG_M + std::min<uint64_t>(d.experts, sk) + 1;
-    const uint64_t si = std::max<uint64_t>(1, S * SI);
-    uint64_t b = 4 * (3 * S * H + S * d.experts + 2 * sk + S + sk * d.inter + si);  // xin, out, xn, logits, ..
-    if (SI) b += 4 * (2 * S * SI + S * H + S);  // the shared expert's gate, up, down rows and gate
-    if (S < (uint64_t)kGroupedMinTokens) return b;
-    b += 4 * (2 * (uint64_t)d.experts + 1 + 3 * sk + 2 * mt + 1 + sk * H + std::max<uint64_t>(1, S * H));
-    if (g.prefill_fp8)  // three E4M3 terms and their exponents
-        b += 3 * (S * H + sk * d.inter) + 3 * (S * H + sk * d.inter) / 32 +
-             std::max<uint64_t>(1, 3 * S * SI) + std::max<uint64_t>(1, 3 * S * SI / 32);
-    else  // f16 hi + lo splits
-        b += 2 * (2 * S * H + 2 * sk * d.inter + 2 * si);
-    return b;
-}
-}  // namespace
+// ---- HBM plan (budget.plan, budget.zig:184-264, for one GPU's HBM): cz_plan.h
+static_assert(cz::kPlanTileRows == CZ_GG_M && cz::kPlanGroupedMinTokens == (uint32_t)kGroupedMinTokens,
+              "the plan's scratch count follows the forward's regimes");
 
 extern "C" int colizig_hip_plan_hbm(const colizig_dims *dims, uint32_t layers, uint64_t hbm_budget,
                                     uint32_t max_tokens, colizig_hbm_plan *out) {
@@ -3315,47 +3308,13 @@ extern "C" int colizig_hip_plan_hbm(const colizig_dims *dims, uint32_t layers, u
     if (!dims || !out || layers == 0 || dims->experts == 0 || dims->topk == 0 || dims->hidden == 0 ||
         dims->inter == 0)
         return -1;
-    const colizig_dims d = *dims;
     if (hbm_budget == 0) {
         std::lock_guard<std::recursive_mutex> lk(g_mu);
         size_t freeb = 0, totalb = 0;
         if (!g.inited || hipMemGetInfo(&freeb, &totalb) != hipSuccess) return -1;
         hbm_budget = freeb - freeb / 8;
     }
-    colizig_hbm_plan p{};
-    p.hbm_budget = hbm_budget;
-    const uint64_t H = d.hidden, nbH = nblk(d.hidden);
-    p.per_expert_bytes = (3ull * d.inter * H + 12ull * nblk(d.inter) * nbH + 15) / 16 * 16;
-    p.per_layer_fixed = 4ull * d.experts * H + 8ull * d.experts + 4ull * d.experts;
-    if (d.shared_inter) p.per_layer_fixed += 3ull * d.shared_inter * H + 12ull * nblk(d.shared_inter) * nbH + 4 * H;
-    p.scratch = work_bytes(d, std::max<uint32_t>(1, max_tokens));
-    p.fixed_resident = (uint64_t)layers * p.per_layer_fixed + p.scratch;
-    const uint64_t all_experts = (uint64_t)layers * d.experts;
-    if (p.fixed_resident > hbm_budget) {
-        snprintf(p.reason, sizeof p.reason, "the resident routers, shared experts and scratch exceed the HBM budget");
-    } else if (p.fixed_resident + all_experts * p.per_expert_bytes <= hbm_budget) {
-        p.all_resident = 1;
-        p.expert_bytes = all_experts * p.per_expert_bytes;
-        p.expert_cap = d.experts;
-        for (uint32_t c : kCapLadder)
-            if (c <= p.expert_cap) { p.ladder_cap = c; break; }
-        p.fits = 1;
-    } else {
-        const uint64_t slots = std::min<uint64_t>((hbm_budget - p.fixed_resident) / p.per_expert_bytes, all_experts);
-        if (slots < d.topk) {
-            snprintf(p.reason, sizeof p.reason, "the expert pool would hold %llu experts, fewer than top-k %u",
-                     (unsigned long long)slots, d.topk);
-        } else {
-            p.pool_slots = (uint32_t)std::min<uint64_t>(slots, 1u << 24);
-            p.expert_bytes = (uint64_t)p.pool_slots * p.per_expert_bytes;
-            p.expert_cap = p.pool_slots / layers;
-            for (uint32_t c : kCapLadder)
-                if (c <= p.expert_cap) { p.ladder_cap = c; break; }
-            p.fits = 1;
-        }
-    }
-    p.total = p.fixed_resident + p.expert_bytes;
-    *out = p;
+    *out = cz::plan_hbm(*dims, layers, hbm_budget, max_tokens, g.prefill_fp8);
     return 0;
 }
 

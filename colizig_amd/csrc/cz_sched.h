@@ -107,9 +107,18 @@ class Scheduler {
     SchedStats st_;
 };
 
+// predict.zig:12-17: one predicted expert with its confidence and the
+// number of layers until it is expected to be used.
+struct PrefetchPrediction {
+    uint32_t layer = 0, expert = 0;
+    float confidence = 0.0f;
+    uint32_t expected_use_distance = 0;
+};
+
 // predict.zig:19-27: of every routed id, whether the prediction held it.
 struct PredStats {
     uint64_t predicted = 0, correct = 0;
+    double accuracy() const { return predicted == 0 ? 0.0 : (double)correct / (double)predicted; }
     void score(const std::vector<uint32_t> &pred, const uint32_t *ids, size_t n) {
         for (size_t i = 0; i < n; ++i) {
             predicted++;
@@ -130,6 +139,17 @@ class LastTokenPredictor {
         static const std::vector<uint32_t> none;
         const auto it = last_.find(layer);
         return it == last_.end() ? none : it->second;
+    }
+
+    // predict.zig:61-72: the prediction as rows of at most max, each with
+    // the predictor's accuracy so far as its confidence (at least 0.1) and
+    // an expected use distance of one layer; returns the rows written.
+    size_t predict_scored(uint32_t layer, PrefetchPrediction *out, size_t max) const {
+        const std::vector<uint32_t> &ids = predict(layer);
+        const float conf = (float)std::max(0.1, st_.accuracy());
+        const size_t n = std::min(ids.size(), max);
+        for (size_t i = 0; i < n; ++i) out[i] = PrefetchPrediction{layer, ids[i], conf, 1u};
+        return n;
     }
 
     void record(uint32_t layer, const uint32_t *ids, size_t n) {

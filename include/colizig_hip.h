@@ -406,6 +406,17 @@ void colizig_hip_predictor_destroy(int64_t h);
 int colizig_hip_predictor_record(int64_t h, uint32_t layer, const uint32_t *ids, uint32_t n);
 int colizig_hip_predictor_predict(int64_t h, uint32_t layer, uint32_t *out, uint32_t max);
 int colizig_hip_predictor_stats(int64_t h, uint64_t *predicted, uint64_t *correct);
+/* predictScored (predict.zig:61-72): the prediction of `layer` as at most
+ * max (<= 64) rows, each with the predictor's accuracy so far as its
+ * confidence (at least 0.1) and an expected use distance of 1; returns the
+ * rows written, or -1 for an unknown handle. */
+typedef struct colizig_prefetch_prediction {
+    uint32_t layer;
+    uint32_t expert;
+    float confidence;
+    uint32_t expected_use_distance;
+} colizig_prefetch_prediction;
+int colizig_hip_predictor_predict_scored(int64_t h, uint32_t layer, colizig_prefetch_prediction *out, uint32_t max);
 
 /* ---- HBM plan (budget.plan, src/runtime/budget.zig:59-264, for HBM) ------
  * Where a model's MoE bytes go on one GPU: every layer keeps its router (f32

@@ -147,3 +147,44 @@ def test_last_token_predictor_keeps_topk():
         assert _predict(h, 1) == [1, 2, 3]
     finally:
         hip.colizig_hip_predictor_destroy(h)
+
+
+class PrefetchPrediction(ctypes.Structure):
+    _fields_ = [("layer", ctypes.c_uint32), ("expert", ctypes.c_uint32), ("confidence", ctypes.c_float),
+                ("expected_use_distance", ctypes.c_uint32)]
+
+
+def _scored(h, layer, k):
+    rows = (PrefetchPrediction * k)()
+    n = _lib.hip().colizig_hip_predictor_predict_scored(h, layer, rows, k)
+    assert n >= 0
+    return [(r.layer, r.expert, r.confidence, r.expected_use_distance) for r in rows[:n]]
+
+
+def test_predict_scored_rows():
+    """predict.zig:112-124 restated: after recording [1, 2, 3] at layer 1
+    with topk 3, predictScored gives three rows for layer 1, row 1 naming
+    expert 2.  The confidence is the accuracy so far with a floor of 0.1
+    (predict.zig:63), the expected use distance 1, and a short buffer takes
+    the first rows only."""
+    hip = _lib.hip()
+    h = hip.colizig_hip_predictor_create(3)
+    try:
+        _record(h, 1, [1, 2, 3])
+        rows = _scored(h, 1, 3)
+        assert len(rows) == 3
+        assert rows[0][0] == 1 and rows[1][1] == 2
+        assert [r[1] for r in rows] == [1, 2, 3]
+        # nothing scored yet (the first record had no prediction): accuracy 0 -> the 0.1 floor
+        assert all(abs(r[2] - np.float32(0.1)) == 0 and r[3] == 1 for r in rows)
+        assert _scored(h, 0, 3) == []  # no prediction for layer 0
+        assert len(_scored(h, 1, 2)) == 2
+        # every recorded id counts as predicted, the first record's three
+        # included (predict.zig:79-88): 2 right of 6 -> accuracy 1/3
+        _record(h, 1, [1, 2, 7])
+        rows = _scored(h, 1, 3)
+        assert [r[1] for r in rows] == [1, 2, 7]
+        assert all(r[2] == np.float32(2.0 / 6.0) for r in rows)
+        assert hip.colizig_hip_predictor_predict_scored(987654321, 1, None, 0) == -1
+    finally:
+        hip.colizig_hip_predictor_destroy(h)
