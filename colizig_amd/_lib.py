@@ -110,6 +110,7 @@ SIGNATURES = {
     "colizig_hip_layer_stream_from_host": (ctypes.c_int, [ctypes.c_uint32, vp, vp]),
     "colizig_hip_stream_decode": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_int, ctypes.c_float]),
     "colizig_hip_stream_stats": (ctypes.c_int, [c_u64p, ctypes.c_int]),
+    "colizig_hip_stream_stats_reset": (ctypes.c_int, []),
     "colizig_hip_stream_pool_free": (ctypes.c_int, []),
     "colizig_hip_set_prefill_fp8": (ctypes.c_int, [ctypes.c_int]),
     "colizig_hip_work_bytes": (ctypes.c_int, [c_u64p]),

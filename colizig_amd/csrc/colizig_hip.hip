@@ -156,7 +156,8 @@ struct StreamPool {
     uint32_t nslots = 0;
     std::vector<uint64_t> key;         // 1 + (layer << 32 | expert), 0 = free
     std::vector<uint64_t> used;        // LRU clock of the last use (or fill)
-    std::vector<uint8_t> prefetched;   // filled by prefetch, not used since
+    std::vector<uint32_t> prefetched;  // stats epoch + 1 of a prefetch fill not used since (0: none)
+    uint32_t stats_epoch = 0;          // colizig_hip_stream_stats_reset opens a new one
     std::vector<uint32_t> pin_epoch;   // slot is needed by the layer in flight
     std::unordered_map<uint64_t, uint32_t> where;
     uint64_t clock = 0;
@@ -2401,7 +2402,7 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
     if (P.key[i] != 0) {
         P.where.erase(P.key[i]);
         P.evictions++;
-        if (P.prefetched[i]) P.prefetch_wasted++;
+        if (P.prefetched[i] == P.stats_epoch + 1) P.prefetch_wasted++;  // issued in this stats window
     }
     uint8_t *dst = slot_w(i);
     if (L.host_packed) {
@@ -2419,7 +2420,7 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
     P.key[i] = pool_key(layer, e);
     P.where[P.key[i]] = i;
     P.used[i] = ++P.clock;
-    P.prefetched[i] = prefetch ? 1 : 0;
+    P.prefetched[i] = prefetch ? P.stats_epoch + 1 : 0;
     if (prefetch) P.prefetch_issued++;
     return 0;
 }
@@ -2443,7 +2444,7 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
             const uint32_t i = it->second;
             P.hits++;
             if (P.prefetched[i]) {
-                P.prefetch_hits++;
+                if (P.prefetched[i] == P.stats_epoch + 1) P.prefetch_hits++;  // issued in this stats window
                 P.prefetched[i] = 0;
             }
             P.used[i] = ++P.clock;
@@ -3130,6 +3131,26 @@ extern "C" int colizig_hip_stream_evict_all(void) {
     pool_log(kOpClear, 0, 0, 0);
     for (auto &kv : g.layers)
         if (kv.second.streamed()) std::fill(kv.second.slot_map.begin(), kv.second.slot_map.end(), -1);
+    return 0;
+}
+
+// Opens a new statistics window: every counter of colizig_hip_stream_stats
+// restarts at 0 (the scheduler's queue peak at the queue's current length),
+// and a prefetch counts as a hit or as wasted only in the window that issued
+// it.  The pool's contents, LRU order and predictions are kept.  0, or -1
+// without a pool.
+extern "C" int colizig_hip_stream_stats_reset(void) {
+    CsrGuard csr;
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    StreamPool &P = g.pool;
+    if (!g.inited || !P.on) return -1;
+    P.stats_epoch++;
+    P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
+        P.bytes_h2d = 0;
+    P.next_stats = cz::PredStats{};
+    P.tok_stats = cz::PredStats{};
+    P.last_pred.reset_stats();
+    P.sched.reset_stats();
     return 0;
 }
 

@@ -95,6 +95,12 @@ class Scheduler {
 
     void clear() { q_.clear(); }
 
+    // Restarts the counters (the peak at the current queue length).
+    void reset_stats() {
+        st_ = SchedStats{};
+        st_.queue_peak = q_.size();
+    }
+
    private:
     struct Entry {
         ExpertKey key;
@@ -163,6 +169,7 @@ class LastTokenPredictor {
     }
 
     const PredStats &stats() const { return st_; }
+    void reset_stats() { st_ = PredStats{}; }
     void set_topk(size_t topk) { topk_ = topk; }
 
    private:

@@ -361,6 +361,12 @@ int colizig_hip_stream_evict_all(void);
  * upgraded, rejected_full, serviced HIGH / MEDIUM / LOW, cancelled,
  * queue_peak; token-level prediction: predicted, correct. */
 int colizig_hip_stream_stats(uint64_t *out, int n);
+/* Opens a new statistics window: every counter above restarts at 0 (the
+ * scheduler's queue peak at the queue's current length), and a prefetch
+ * counts as a hit or as wasted only in the window that issued it.  The
+ * pool's contents, LRU order and predictions are kept.  0, or -1 without a
+ * pool.  No counterpart in the reference. */
+int colizig_hip_stream_stats_reset(void);
 
 /* Routing prediction for prefetch at one token: bit 0, the next streamed
  * layer's routing from the current layer's router input (its router and

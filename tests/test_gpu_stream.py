@@ -151,3 +151,39 @@ def test_stream_priors_warm_the_pool(pool):
     st2 = moe.stream_stats()
     assert st2["prefetch_hits"] > st1["prefetch_hits"]
     say(f"  warmed {warmed} of {hot}; prefetch hits {st2['prefetch_hits'] - st1['prefetch_hits']}")
+
+
+def test_stream_stats_window(pool):
+    """colizig_hip_stream_stats_reset opens a window with its own counters:
+    the warmed pool's prefetches were issued before the window, so the
+    window's hits on them are hits but not prefetch hits; inside the window
+    prefetch hits plus wasted never exceed the prefetches issued, every miss
+    and prefetch is one load, and the queue peak is the window's."""
+    from colizig_amd.usage import ExpertUsage
+    say("stream stats window after a warm start")
+    nl = 2
+    _layers(2600, 2700, nl, seed=61)
+    hip = _lib.hip()
+    xs = moe.DeviceBuffer(H * 4)
+    xs.upload(synth.hidden_states(1, H, seed=61))
+    for _ in range(4):
+        assert hip.colizig_hip_stream_decode(2700, nl, xs.ptr, 1, 1e-6) == 0, _lib.last_error()
+    assert hip.colizig_hip_sync() == 0
+    u = ExpertUsage.from_pool(2700, nl, E)
+    assert hip.colizig_hip_stream_evict_all() == 0
+    warmed = u.warm_pool(2700)
+    assert warmed > 0
+    assert hip.colizig_hip_stream_stats_reset() == 0
+    st = moe.stream_stats()
+    assert all(st[k] == 0 for k in st if k not in ("slots", "resident", "sched_queue_peak"))
+    steps = 6
+    for _ in range(steps):
+        assert hip.colizig_hip_stream_decode(2700, nl, xs.ptr, 1, 1e-6) == 0, _lib.last_error()
+    assert hip.colizig_hip_sync() == 0
+    st = moe.stream_stats()
+    say(f"  {st}")
+    assert st["hits"] + st["misses"] == steps * nl * K
+    assert st["hits"] > 0  # the warmed experts
+    assert st["prefetch_hits"] + st["prefetch_wasted"] <= st["prefetch_issued"]
+    assert st["loads"] == st["misses"] + st["prefetch_issued"]
+    assert st["bytes_h2d"] == st["loads"] * SLOT
