@@ -27,6 +27,8 @@
 
 #include "cz_kernels.h"
 
+#include <type_traits>
+
 typedef _Float16 cz_half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 cz_half4 __attribute__((ext_vector_type(4)));
 typedef float cz_float16v __attribute__((ext_vector_type(16)));
@@ -312,6 +314,27 @@ __device__ __forceinline__ cz_half8 cz_fp8x8_to_f16(uint32_t w0, uint32_t w1) {
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
     return r;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over the bytes from p on (offsets below 2 GiB; gfx9
+// word 3: 32-bit data format), p read from the first lane so the resource
+// lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cz_rsrc(const void *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// A pointer that every lane of the wave holds, read from the first lane so
+// that it lives in scalar registers.
+__device__ __forceinline__ const uint8_t *cz_uniform_ptr(const uint8_t *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (const uint8_t *)(((uint64_t)hi << 32) | lo);
 }
 
 enum GGMode { GG_GATEUP = 0, GG_DOWN = 1 };
@@ -652,14 +675,25 @@ __global__ __launch_bounds__(256) void k_quant3(const float *__restrict__ src, u
 
 typedef int cz_i8x32 __attribute__((ext_vector_type(8)));
 
-// A tile of one K block in LDS for k_gg8: 3 term planes x CZ_GG_M rows x 128
-// bytes (8 chunks of 16 B; chunk c of row r at c ^ (r & 7)), then the
-// exponents: 3 planes x CZ_GG_M rows x 4 bytes.
-#define CZ_GG8_APLANE (CZ_GG_M * 128)
+// A tile of one K block in LDS for k_gg8: 3 term planes x CZ_GG_M rows of 128
+// bytes (8 chunks of 16 B) CZ_GG8_ALD bytes apart, then the exponents: 3
+// planes x CZ_GG_M rows x 4 bytes.
+#define CZ_GG8_ALD 144  // LDS bytes per A row (128 + 16: the rows one read phase touches start in distinct bank groups)
+#define CZ_GG8_APLANE (CZ_GG_M * CZ_GG8_ALD)
 #define CZ_GG8_EOFF (3 * CZ_GG8_APLANE)
-#define CZ_GG8_HT 36  // floats per row of a wave's h tile in its weight stage (144 B: float4-aligned)
-__device__ __forceinline__ uint32_t cz_gg8_off(uint32_t r, uint32_t c) { return r * 128u + ((c ^ (r & 7u)) << 4); }
+#define CZ_GG8_STAGE (CZ_GG8_EOFF + 3 * CZ_GG_M * 4)
+#define CZ_GG8_HT 36  // floats per row of a wave's h tile in its weight buffer (144 B: float4-aligned)
+static_assert(32 * CZ_GG8_HT * 4 <= 64 * CZ_GG_WLD, "a wave's h tile fits in its weight buffer");
+__device__ __forceinline__ uint32_t cz_gg8_off(uint32_t r, uint32_t c) { return r * CZ_GG8_ALD + (c << 4); }
 
+// Grouped GEMM on FP8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): one M-tile
+// (32 rows of one expert) x cz_gg_cols() output columns per workgroup, the
+// work items and their XCD mapping as in k_gg.  A K block (128 columns) is
+// the A tile's three E4M3 term planes with their E8M0 exponents (shared by
+// the four waves, in LDS) and each wave's 64 weight rows (its own LDS
+// buffer).  Loads run two K blocks ahead in two register sets, written to
+// LDS after the block before them is multiplied; one barrier per block.
+// Two workgroups per CU.
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGProblem PS) {
     constexpr uint32_t NCOL = cz_gg_cols<MODE>();
@@ -668,8 +702,7 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
     const bool sh = blockIdx.x < ns8;
     if (sh && blockIdx.x >= ns) return;  // block-uniform
     const GGProblem P = sh ? PS : PR;
-    __shared__ __align__(16) uint8_t lds0[CZ_GG8_EOFF + 3 * CZ_GG_M * 4];
-    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_WLD];
+    __shared__ __align__(16) uint8_t lds0[2][CZ_GG8_STAGE];
     __shared__ uint32_t s_rowsrc[CZ_GG_M];
     __shared__ uint32_t s_rowdst[CZ_GG_M];
 
@@ -704,11 +737,11 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
     // A staging: thread t moves chunk t%8 of row t/8 of each term plane;
     // threads < 96 move one 4-byte exponent word (plane t/32, row t%32)
     const uint32_t ar = tid >> 3, ac = tid & 7u;
-    const uint64_t a_src = (uint64_t)s_rowsrc[ar] * P.Kd + ac * 16u;
+    const uint32_t a_src = s_rowsrc[ar] * P.Kd + ac * 16u;  // < 4 GiB: rows x Kd of one term plane
     const uint32_t a_dst = cz_gg8_off(ar, ac);
     const uint32_t nbe = P.Kd / 32u;
-    const uint32_t ep = tid >> 5, er = tid & 31u;
-    const uint64_t e_src = ep * P.ae_plane + (uint64_t)s_rowsrc[min(er, (uint32_t)CZ_GG_M - 1)] * nbe;
+    const uint32_t ep = min(tid >> 5, 2u), er = tid & 31u;
+    const uint32_t e_src = ep * (uint32_t)P.ae_plane + s_rowsrc[min(er, (uint32_t)CZ_GG_M - 1)] * nbe;
 
     const uint64_t sl = P.routed ? cz_slot(G.L, e) : 0;
     const uint8_t *W0 = P.w0 + sl * P.w_stride;
@@ -725,9 +758,20 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
         wbase[m] = W0 + moff + (uint64_t)nb * P.Kd;
         srow[m] = S0 + soff + (uint64_t)(nb / CZ_BLOCK) * P.nbK;
     }
+    // Weights: each wave stages its own 64 rows (32 per subtile) of a K block
+    // in its LDS buffer (rows CZ_GG_WLD bytes apart); lane l loads 16 bytes
+    // (l % 8) of rows l / 8 + 8 i, so one wave instruction reads 8 whole
+    // 128-byte row segments.  Every load is a buffer load: a wave-uniform
+    // resource (the block of weight rows, a term plane), a 32-bit lane
+    // offset that does not change along K, and the K block's offset (plus
+    // 8 i rows) as the scalar offset.
+    const uint32_t rl = lane & 31u, hh = lane >> 5;
+    __shared__ __align__(16) uint8_t ldsw[4][64 * CZ_GG_WLD];
     uint8_t *lw = ldsw[wave];
-    const uint32_t wl_off = (lane >> 3) * P.Kd + (lane & 7u) * 16u;
+    const __amdgpu_buffer_rsrc_t rw0 = cz_rsrc(wbase[0]), rw1 = cz_rsrc(wbase[1]);
+    const uint32_t w_lane = (lane >> 3) * P.Kd + (lane & 7u) * 16u;
     const uint32_t wl_lds = (lane >> 3) * CZ_GG_WLD + (lane & 7u) * 16u;
+    const int r8 = (int)(8u * P.Kd);
 
     cz_float16v acc[2];
 #pragma unroll
@@ -736,62 +780,81 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
         for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
     float cur[2] = {0.0f, 0.0f};
     const uint32_t nkb = P.Kd / CZ_GG_KB;
-    const uint8_t *gl0 = wbase[0] + wl_off, *gl1 = wbase[1] + wl_off;
-    const uint64_t r8 = 8ull * P.Kd;
-    uint4 x0, x1, x2, x3, x4, x5, x6, x7, q0, q1, q2;
-    uint32_t ev = 0;
-#define CZ_GG8_LOAD(kb_)                                                        \
-    {                                                                           \
-        const uint64_t ko_ = (uint64_t)(kb_) * CZ_GG_KB;                        \
-        q0 = *(const uint4 *)(P.aq + a_src + ko_);                              \
-        q1 = *(const uint4 *)(P.aq + P.aq_plane + a_src + ko_);                 \
-        q2 = *(const uint4 *)(P.aq + 2 * P.aq_plane + a_src + ko_);             \
-        if (tid < 96) ev = *(const uint32_t *)(P.ae + e_src + (kb_) * 4u);      \
-        x0 = *(const uint4 *)(gl0 + ko_);                                       \
-        x1 = *(const uint4 *)(gl0 + r8 + ko_);                                  \
-        x2 = *(const uint4 *)(gl0 + 2 * r8 + ko_);                              \
-        x3 = *(const uint4 *)(gl0 + 3 * r8 + ko_);                              \
-        x4 = *(const uint4 *)(gl1 + ko_);                                       \
-        x5 = *(const uint4 *)(gl1 + r8 + ko_);                                  \
-        x6 = *(const uint4 *)(gl1 + 2 * r8 + ko_);                              \
-        x7 = *(const uint4 *)(gl1 + 3 * r8 + ko_);                              \
-    }
-#define CZ_GG8_STORE()                                                          \
-    {                                                                           \
-        *(uint4 *)(lds0 + a_dst) = q0;                                          \
-        *(uint4 *)(lds0 + CZ_GG8_APLANE + a_dst) = q1;                          \
-        *(uint4 *)(lds0 + 2 * CZ_GG8_APLANE + a_dst) = q2;                      \
-        if (tid < 96) *(uint32_t *)(lds0 + CZ_GG8_EOFF + 4u * tid) = ev;        \
-        uint8_t *d_ = lw + wl_lds;                                              \
-        *(uint4 *)(d_) = x0;                                                    \
-        *(uint4 *)(d_ + 1 * 8 * CZ_GG_WLD) = x1;                                 \
-        *(uint4 *)(d_ + 2 * 8 * CZ_GG_WLD) = x2;                                 \
-        *(uint4 *)(d_ + 3 * 8 * CZ_GG_WLD) = x3;                                 \
-        *(uint4 *)(d_ + 4 * 8 * CZ_GG_WLD) = x4;                                 \
-        *(uint4 *)(d_ + 5 * 8 * CZ_GG_WLD) = x5;                                 \
-        *(uint4 *)(d_ + 6 * 8 * CZ_GG_WLD) = x6;                                 \
-        *(uint4 *)(d_ + 7 * 8 * CZ_GG_WLD) = x7;                                 \
-    }
-    CZ_GG8_LOAD(0)
-    CZ_GG8_STORE()
-    CZ_GG8_LOAD(min(1u, nkb - 1))
-    __syncthreads();
-    const uint32_t rl = lane & 31u, hh = lane >> 5;
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        // block scales folded into acc as in k_gg (cz_gg_rescale): acc is
-        // rescaled by cur / s, and a zero-scale block's weights are masked
-        // to +0 as they are read
-        uint32_t keep[2];
+    // Two K blocks ahead: while block kb is multiplied (A from LDS stage
+    // kb % 2, weights from the wave's LDS buffer), the A rows and weights of
+    // blocks kb + 1 and kb + 2 are in flight into register sets (kb + 1) % 2
+    // and kb % 2.  After block kb's products, block kb + 1 goes from its
+    // registers to LDS.  One barrier per K block.
+    struct WSet {
+        u32x4 v[8];
+    };
+    struct ASet {
+        u32x4 q[3];
+        uint32_t ev;
+    };
+    const __amdgpu_buffer_rsrc_t ra0 = cz_rsrc(P.aq), ra1 = cz_rsrc(P.aq + P.aq_plane),
+                                 ra2 = cz_rsrc(P.aq + 2 * P.aq_plane), re0 = cz_rsrc(P.ae);
+    WSet w0, w1;
+    ASet a0, a1;
+    // the register sets by compile-time index (distinct variables, so they stay in registers)
+    auto wset = [&](auto I) __attribute__((always_inline)) -> WSet & {
+        if constexpr (decltype(I)::value == 0) return w0;
+        else return w1;
+    };
+    auto aset = [&](auto I) __attribute__((always_inline)) -> ASet & {
+        if constexpr (decltype(I)::value == 0) return a0;
+        else return a1;
+    };
+    auto load = [&](uint32_t kb, ASet &as, WSet &ws) __attribute__((always_inline)) {
+        const int ko = (int)(kb * CZ_GG_KB);
+        as.q[0] = __builtin_amdgcn_raw_buffer_load_b128(ra0, a_src, ko, 0);
+        as.q[1] = __builtin_amdgcn_raw_buffer_load_b128(ra1, a_src, ko, 0);
+        as.q[2] = __builtin_amdgcn_raw_buffer_load_b128(ra2, a_src, ko, 0);
+        as.ev = __builtin_amdgcn_raw_buffer_load_b32(re0, e_src, (int)(kb * 4u), 0);  // threads >= 96: a copy, never stored
+        u32x4 *w = ws.v;
+        w[0] = __builtin_amdgcn_raw_buffer_load_b128(rw0, w_lane, ko, 0);
+        w[1] = __builtin_amdgcn_raw_buffer_load_b128(rw0, w_lane, ko + r8, 0);
+        w[2] = __builtin_amdgcn_raw_buffer_load_b128(rw0, w_lane, ko + 2 * r8, 0);
+        w[3] = __builtin_amdgcn_raw_buffer_load_b128(rw0, w_lane, ko + 3 * r8, 0);
+        w[4] = __builtin_amdgcn_raw_buffer_load_b128(rw1, w_lane, ko, 0);
+        w[5] = __builtin_amdgcn_raw_buffer_load_b128(rw1, w_lane, ko + r8, 0);
+        w[6] = __builtin_amdgcn_raw_buffer_load_b128(rw1, w_lane, ko + 2 * r8, 0);
+        w[7] = __builtin_amdgcn_raw_buffer_load_b128(rw1, w_lane, ko + 3 * r8, 0);
+    };
+    // A rows to an LDS stage, the wave's weights to its buffer (the wave's
+    // DS operations stay in program order: its reads of the previous block
+    // are done before these writes)
+    auto store = [&](uint8_t *st, const ASet &as, const WSet &ws) __attribute__((always_inline)) {
+        *(u32x4 *)(st + a_dst) = as.q[0];
+        *(u32x4 *)(st + CZ_GG8_APLANE + a_dst) = as.q[1];
+        *(u32x4 *)(st + 2 * CZ_GG8_APLANE + a_dst) = as.q[2];
+        if (tid < 96) *(uint32_t *)(st + CZ_GG8_EOFF + 4u * tid) = as.ev;
+        uint8_t *d = lw + wl_lds;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) *(u32x4 *)(d + p * 8 * CZ_GG_WLD) = ws.v[p];
+    };
+    // block scales folded into acc as in k_gg (cz_gg_rescale): before block
+    // kb's products acc is rescaled by cur / s_kb, and a zero-scale block's
+    // weights are cleared.  The factors of block kb + 1 are worked out while
+    // block kb's MFMAs run.
+    float rr[2];
+    uint32_t keep[2];
+    auto scales = [&](uint32_t kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             const float sc = cz_const_f32(srow[m] + kb);
             const bool zero = sc == 0.0f;
-            const float rr = (zero || cur[m] == 0.0f) ? 1.0f : cur[m] / sc;
+            rr[m] = (zero || cur[m] == 0.0f) ? 1.0f : cur[m] / sc;
             cur[m] = zero ? cur[m] : sc;
             keep[m] = zero ? 0u : ~0u;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[m][i] *= rr;
         }
+    };
+    auto block = [&](uint32_t kb, const uint8_t *st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[m][i] *= rr[m];
+        const uint32_t kp[2] = {keep[0], keep[1]};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             // the wave's weights in MFMA layout: subtile m, K half kk: row 32m
@@ -801,40 +864,71 @@ __global__ __launch_bounds__(256, 2) void k_gg8(GroupArgs G, GGProblem PR, GGPro
             for (int m = 0; m < 2; ++m) {
                 const uint8_t *rowp = lw + (32u * m + rl) * CZ_GG_WLD + 64u * kk + 16u * hh;
                 const uint4 lo = *(const uint4 *)rowp, hi = *(const uint4 *)(rowp + 32u);
-                const uint32_t k_ = keep[m];
+                const uint32_t k_ = kp[m];
                 bm[m] = cz_i8x32{(int)(lo.x & k_), (int)(lo.y & k_), (int)(lo.z & k_), (int)(lo.w & k_),
                                  (int)(hi.x & k_), (int)(hi.y & k_), (int)(hi.z & k_), (int)(hi.w & k_)};
             }
 #pragma unroll
             for (int tt = 0; tt < 3; ++tt) {
-                const uint8_t *pl = lds0 + tt * CZ_GG8_APLANE;
+                const uint8_t *pl = st + tt * CZ_GG8_APLANE;
                 const uint4 lo = *(const uint4 *)(pl + cz_gg8_off(rl, 4u * kk + hh));
                 const uint4 hi = *(const uint4 *)(pl + cz_gg8_off(rl, 4u * kk + 2u + hh));
                 const cz_i8x32 am = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z,
                                      (int)hi.w};
                 // exponent of row lane%32, group 2 kk + lane/32 of this K block
-                const int sa = (int)lds0[CZ_GG8_EOFF + (tt * CZ_GG_M + rl) * 4u + 2u * kk + hh];
+                const int sa = (int)st[CZ_GG8_EOFF + (tt * CZ_GG_M + rl) * 4u + 2u * kk + hh];
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
                     acc[m] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(am, bm[m], acc[m], 0, 0, 0, sa, 0, 127);
             }
+            // the K half's products stay here: without a use, the compiler
+            // sinks pure MFMAs past the next block's loads and barrier
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+            if (kk == 0 && kb + 1 < nkb) scales(kb + 1);  // beside the second half's MFMAs
         }
-        if (kb + 1 < nkb) {  // block-uniform
-            __syncthreads();
-            CZ_GG8_STORE()
-            CZ_GG8_LOAD(min(kb + 2, nkb - 1))
-            __syncthreads();
-        }
+    };
+    // one K block; S = kb % 2 names the register sets and the A stage at
+    // compile time.  Every step issues the loads of block kb + 2 (in the
+    // last two steps: the last block again, never stored), so every path
+    // through the loop issues the same loads and the waits the compiler
+    // places count exactly the loads issued after the ones they wait for.
+    auto step = [&](uint32_t kb, auto Sc, auto CLc) __attribute__((always_inline)) {
+        constexpr int S = decltype(Sc)::value;
+        using Cur = std::integral_constant<int, S>;
+        using Nxt = std::integral_constant<int, 1 - S>;
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // stage S holds A(kb); every wave is done with stage 1 - S
+        load(decltype(CLc)::value ? min(kb + 2, nkb - 1) : kb + 2, aset(Cur{}), wset(Cur{}));
+        block(kb, lds0[S]);
+        if (kb + 1 < nkb) store(lds0[1 - S], aset(Nxt{}), wset(Nxt{}));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using IN = std::integral_constant<bool, false>;  // block kb + 2 exists
+    using CL = std::integral_constant<bool, true>;   // clamp to the last block
+    load(0, a0, w0);
+    load(min(1u, nkb - 1), a1, w1);
+    store(lds0[0], a0, w0);
+    scales(0);
+    uint32_t kb = 0;
+    for (; kb + 4 <= nkb; kb += 2) {  // every load of these two steps is in range
+        step(kb, I0{}, IN{});
+        step(kb + 1, I1{}, IN{});
     }
-#undef CZ_GG8_LOAD
-#undef CZ_GG8_STORE
+    // the last 1 .. 3 blocks; each step is reached only through the one before
+    step(kb, I0{}, CL{});
+    if (kb + 1 < nkb) {
+        step(kb + 1, I1{}, CL{});
+        if (kb + 2 < nkb) step(kb + 2, I0{}, CL{});
+    }
     if constexpr (MODE == GG_GATEUP) {
         // h = silu(g) * u of the wave's 32 rows x 32 columns (one 32-column
         // group) goes through the wave's own weight stage (its DS operations
         // stay in program order, so no barrier) to k_quant3's layout, 8 lanes
         // per row with four columns each, and leaves as the three E4M3 terms
         // of the down GEMM's A rows: the bytes k_quant3 makes of the f32 rows
-        float *ht = reinterpret_cast<float *>(lw);  // [32][CZ_GG8_HT], 4.5 KB of the 9 KB stage
+        float *ht = reinterpret_cast<float *>(lw);  // [32][CZ_GG8_HT], 4.5 KB of the wave's 9 KB buffer
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t r = (i / 4) * 8u + (lane >> 5) * 4u + (i % 4);
