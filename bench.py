@@ -42,6 +42,11 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # (the mean over a step's 47 launches with predicted experts and its first).
 LAYER_TRAFFIC_BYTES = int(round((24431.5 * 2.0 + 134.5) * 1024))
 
+# HBM bytes per 512-token prefill step (48 layers x the seven kernels of a
+# layer), measured the same way: 264082.5 KiB fetched and 54035.2 KiB
+# written per layer, the sums of the kernels' per-dispatch means.
+PREFILL_STEP_TRAFFIC_BYTES = int(round(48 * (264082.5 * 2.0 + 54035.2) * 1024))
+
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
 
@@ -374,8 +379,9 @@ def prefill_bench(args) -> None:
         "data": "synthetic (seeded N(0,0.02) weights generated in HBM, N(0,1) hidden states)",
         "config": {**c, "parallelism": "none (1 GPU)", "global_batch": S, "seq_len": S},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "scope": "whole step",
-                     "bytes_per_step": step_bytes},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": PREFILL_STEP_TRAFFIC_BYTES if (S == 512 and NL == 48) else None,
+                     "scope": "whole step", "bytes_per_step": step_bytes},
         "mfma_tflops": round(step_flops / (ms * 1e-3) / 1e12, 2),
         # useful FLOPs / step time against the dense peak of the MFMA in use
         # (FP8 5.0 PFLOP/s, f16 2.5 PFLOP/s; the activation terms multiply the work done)
