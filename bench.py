@@ -99,9 +99,10 @@ def main():
     ap.add_argument("--priors", action="store_true",
                     help="stream: warm the pool from learned priors (.colizig_usage written by an untimed "
                          "previous session of --steps tokens on the same workload) before the timed tokens")
-    ap.add_argument("--predict", type=int, default=2, choices=[0, 1, 2, 3],
+    ap.add_argument("--predict", type=int, default=6, choices=list(range(8)),
                     help="stream: routing prediction for prefetch (bit 0: next layer from the current layer's "
-                         "router input; bit 1: every later layer from the token's first router input); 0: only "
+                         "router input; bit 1: every later layer from the token's first router input; bit 2, "
+                         "with bit 1: the later layers enqueued at once, the host off their path); 0: only "
                          "the last token's routing")
     ap.add_argument("--split-slabs", action="store_true",
                     help="stream: weights and scales in two host slabs (two copies per fill) instead of one packed slab")

@@ -163,16 +163,17 @@ struct StreamPool {
     uint64_t clock = 0;
     uint32_t epoch = 0;
     hipStream_t copy = nullptr;
-    hipEvent_t ev_idx = nullptr, ev_copy = nullptr;
+    hipEvent_t ev_idx = nullptr, ev_copy = nullptr, ev_copy_hi = nullptr;
     uint32_t *h_idx = nullptr;         // pinned routing read-back (host-coherent)
     size_t h_idx_cap = 0;
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
     uint32_t seq = 0;
     // routing prediction (one token), bit 0: the next streamed layer's from
     // the current layer's router input; bit 1: every later streamed layer's
-    // from the chain's first router input.  Device scratch of the predicted
+    // from the chain's first router input; bit 2 (with bit 1): those later
+    // layers in speculative runs (run_spec_layers).  Device scratch of the predicted
     // routing, the picks in host-coherent memory and their sequence numbers.
-    int predict_mode = 2;
+    int predict_mode = 6;
     float *pred_logits = nullptr, *pred_gates = nullptr, *pred_sgate = nullptr;
     uint32_t *pred_idx = nullptr, *pred_tord = nullptr;
     uint32_t *route_count = nullptr;  // the router kernel's block counter (one-token routing), kept at zero
@@ -189,12 +190,17 @@ struct StreamPool {
     uint32_t tseq = 0;
     std::unordered_map<uint32_t, std::vector<uint32_t>> tok_ids;   // layer -> its token-level prediction
     cz::PredStats tok_stats;
-    // copy-stream completion per slot: the event recorded after the slot's
-    // latest fill and that fill's sequence number; the compute stream has
-    // waited for every fill up to waited_seq
+    // Fills go on two copy streams: prefetches on copy, demand fills (a
+    // layer's misses) on copy_hi, so a miss does not queue behind the
+    // prefetches.  Per slot: the event recorded after its latest fill, that
+    // fill's sequence number and its stream.  The compute stream has waited
+    // for every fill of copy stream s up to waited[s] (each stream is in
+    // order).
+    hipStream_t copy_hi = nullptr;
     std::vector<hipEvent_t> slot_ev;
     std::vector<uint64_t> fill_seq;
-    uint64_t fill_counter = 0, waited_seq = 0;
+    std::vector<uint8_t> fill_sid;
+    uint64_t fill_counter = 0, waited[2] = {0, 0};
     cz::LastTokenPredictor last_pred{8};
     cz::Scheduler sched{kSchedCapacity};
     bool log_on = false;
@@ -202,6 +208,14 @@ struct StreamPool {
     // counters (CacheStats, moe.zig:121-139)
     uint64_t hits = 0, misses = 0, loads = 0, evictions = 0, prefetch_issued = 0, prefetch_hits = 0,
              prefetch_wasted = 0, bytes_h2d = 0;
+    // routing prediction bit 2 (with bit 1): the later layers of a token run
+    // with the host off their path (run_spec_layers).  Device stop word, the
+    // run's picks ([layers][K]) and their pinned read-back (stop word first)
+    uint32_t *stop_dev = nullptr, *spec_idx_dev = nullptr, *h_spec = nullptr;
+    size_t spec_cap = 0;               // picks the buffers hold
+    int32_t *spec_tab_dev = nullptr, *h_spec_tab = nullptr;  // the run's slot maps [layers][E], one upload
+    size_t spec_tab_cap = 0;
+    uint64_t spec_layers = 0, spec_stops = 0;  // layers run that way; runs a missing slot stopped
 };
 
 // ---- one-launch-per-layer batch-1 decode (cz_fused.h): its device state.
@@ -1214,17 +1228,21 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (g.fused.err_host) (void)hipHostFree(g.fused.err_host);
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
+    if (P.copy_hi) (void)hipStreamSynchronize(P.copy_hi);
     for (void *p : {(void *)P.base, (void *)P.pred_logits, (void *)P.pred_gates, (void *)P.pred_sgate,
                     (void *)P.pred_idx, (void *)P.pred_tord, (void *)P.route_count, (void *)P.tok_logits, (void *)P.tok_gates,
-                    (void *)P.tok_idx, (void *)P.tok_tord, (void *)P.tok_ptr_dev})
+                    (void *)P.tok_idx, (void *)P.tok_tord, (void *)P.tok_ptr_dev, (void *)P.stop_dev,
+                    (void *)P.spec_idx_dev, (void *)P.spec_tab_dev})
         if (p) (void)hipFree(p);
     for (void *p : {(void *)P.h_idx, (void *)P.h_flag, (void *)P.h_pred, (void *)P.h_pflag, (void *)P.h_tok,
-                    (void *)P.h_tflag, (void *)P.tok_ptr_stage})
+                    (void *)P.h_tflag, (void *)P.tok_ptr_stage, (void *)P.h_spec, (void *)P.h_spec_tab})
         if (p) (void)hipHostFree(p);
     for (hipEvent_t e : P.slot_ev) (void)hipEventDestroy(e);
     if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
     if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
+    if (P.ev_copy_hi) (void)hipEventDestroy(P.ev_copy_hi);
     if (P.copy) (void)hipStreamDestroy(P.copy);
+    if (P.copy_hi) (void)hipStreamDestroy(P.copy_hi);
     (void)hipStreamDestroy(g.stream);
     g.~Ctx();
     new (&g) Ctx();
@@ -2401,24 +2419,36 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
     StreamPool &P = g.pool;
     if (P.key[i] != 0) {
         P.where.erase(P.key[i]);
+        const uint64_t ok = P.key[i] - 1;  // the evicted (layer, expert): no slot any more
+        if (LayerHost *Lo = find_layer((uint32_t)(ok >> 32)))
+            if ((uint32_t)ok < Lo->slot_map.size() && Lo->slot_map[(uint32_t)ok] == (int32_t)i)
+                Lo->slot_map[(uint32_t)ok] = -1;
         P.evictions++;
         if (P.prefetched[i] == P.stats_epoch + 1) P.prefetch_wasted++;  // issued in this stats window
     }
     uint8_t *dst = slot_w(i);
+    const uint8_t sid = prefetch ? 0 : 1;
+    hipStream_t cs = sid ? P.copy_hi : P.copy;
+    // the slot's previous fill went through the other copy stream: this one
+    // waits for it, so two copies never overlap in one slot
+    if (P.fill_seq[i] && P.fill_sid[i] != sid && P.fill_seq[i] > P.waited[P.fill_sid[i]])
+        CZ_CHECK(hipStreamWaitEvent(cs, P.slot_ev[i], 0), -4);
     if (L.host_packed) {
         CZ_CHECK(hipMemcpyAsync(dst, L.host_packed + (uint64_t)e * P.slot_bytes, P.slot_bytes, hipMemcpyHostToDevice,
-                                P.copy), -3);
+                                cs), -3);
     } else {
-        CZ_CHECK(hipMemcpyAsync(dst, L.host_ew + (uint64_t)e * P.w_slot, P.w_slot, hipMemcpyHostToDevice, P.copy), -3);
+        CZ_CHECK(hipMemcpyAsync(dst, L.host_ew + (uint64_t)e * P.w_slot, P.w_slot, hipMemcpyHostToDevice, cs), -3);
         CZ_CHECK(hipMemcpyAsync(dst + P.w_slot, L.host_es + (uint64_t)e * P.s_slot, P.s_slot * sizeof(float),
-                                hipMemcpyHostToDevice, P.copy), -3);
+                                hipMemcpyHostToDevice, cs), -3);
     }
-    CZ_CHECK(hipEventRecord(P.slot_ev[i], P.copy), -4);
+    CZ_CHECK(hipEventRecord(P.slot_ev[i], cs), -4);
     P.fill_seq[i] = ++P.fill_counter;
+    P.fill_sid[i] = sid;
     P.bytes_h2d += P.w_slot + P.s_slot * sizeof(float);
     P.loads++;
     P.key[i] = pool_key(layer, e);
     P.where[P.key[i]] = i;
+    L.slot_map[e] = (int32_t)i;  // a layer's slot map holds every resident expert of it
     P.used[i] = ++P.clock;
     P.prefetched[i] = prefetch ? P.stats_epoch + 1 : 0;
     if (prefetch) P.prefetch_issued++;
@@ -2432,6 +2462,27 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
 // and the compute stream waits for the copy stream only if fills are in
 // flight; otherwise the layer's slot map is uploaded on the copy stream and
 // the compute stream waits for all of it.
+// Stream st waits for the latest fill of each copy stream among `slots`.
+int wait_fills(hipStream_t st, const uint32_t *slots, size_t n) {
+    StreamPool &P = g.pool;
+    uint64_t need[2] = {P.waited[0], P.waited[1]};
+    uint32_t at[2] = {0, 0};
+    for (size_t k = 0; k < n; ++k) {
+        const uint32_t i = slots[k];
+        const uint8_t s = P.fill_sid[i];
+        if (P.fill_seq[i] > need[s]) {
+            need[s] = P.fill_seq[i];
+            at[s] = i;
+        }
+    }
+    for (int s = 0; s < 2; ++s)
+        if (need[s] > P.waited[s]) {
+            CZ_CHECK(hipStreamWaitEvent(st, P.slot_ev[at[s]], 0), -4);
+            P.waited[s] = need[s];
+        }
+    return 0;
+}
+
 int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &sel, hipStream_t st,
                     LayerDev *Ld = nullptr) {
     StreamPool &P = g.pool;
@@ -2468,32 +2519,24 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
     if (Ld && sel.size() <= CZ_SEL_ARGS && P.nslots <= 0x10000u && L.d.experts <= 0x10000u) {
         Ld->sel_n = (uint32_t)sel.size();
         for (size_t k = 0; k < sel.size(); ++k) Ld->sel[k] = sel[k] | ((uint32_t)L.slot_map[sel[k]] << 16);
-        // the compute stream waits for the latest fill of these slots only (the
-        // copy stream is in order: that covers the earlier ones); later
-        // prefetches keep filling underneath
-        uint64_t need = P.waited_seq;
-        uint32_t at = 0;
-        for (uint32_t e : sel) {
-            const uint32_t i = (uint32_t)L.slot_map[e];
-            if (P.fill_seq[i] > need) {
-                need = P.fill_seq[i];
-                at = i;
-            }
-        }
-        if (need > P.waited_seq) {
-            CZ_CHECK(hipStreamWaitEvent(st, P.slot_ev[at], 0), -4);
-            P.waited_seq = need;
-        }
+        // the compute stream waits for the latest fill of these slots on
+        // each copy stream only (each is in order: that covers the earlier
+        // ones); later prefetches keep filling underneath
+        std::vector<uint32_t> slots;
+        for (uint32_t e : sel) slots.push_back((uint32_t)L.slot_map[e]);
+        if (int rc = wait_fills(st, slots.data(), slots.size())) return rc;
     } else {
         // the slot map of this layer: only its selected entries matter (others
         // may be stale and are never read by this layer's kernels); uploaded
         // behind every fill so far, which the compute stream then waits for
         memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
+        CZ_CHECK(hipEventRecord(P.ev_copy_hi, P.copy_hi), -4);  // behind the demand fills too
+        CZ_CHECK(hipStreamWaitEvent(P.copy, P.ev_copy_hi, 0), -4);
         CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
                                 hipMemcpyHostToDevice, P.copy), -3);
         CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
         CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
-        P.waited_seq = P.fill_counter;
+        P.waited[0] = P.waited[1] = P.fill_counter;
     }
     return 0;
 }
@@ -2816,6 +2859,130 @@ int run_streamed_layer(LayerHost &L, uint32_t layer, const float *x, int S, floa
     return 0;
 }
 
+// Buffers of a run of n later layers of E experts and K picks each.
+int ensure_spec(size_t n, uint32_t E, uint32_t K) {
+    StreamPool &P = g.pool;
+    if (!P.stop_dev && hipMalloc(&P.stop_dev, sizeof(uint32_t)) != hipSuccess) return -2;
+    if (P.spec_tab_cap < n * E) {
+        if (P.spec_tab_dev) (void)hipFree(P.spec_tab_dev);
+        if (P.h_spec_tab) (void)hipHostFree(P.h_spec_tab);
+        P.spec_tab_dev = P.h_spec_tab = nullptr;
+        P.spec_tab_cap = 0;
+        if (hipMalloc(&P.spec_tab_dev, n * E * sizeof(int32_t)) != hipSuccess ||
+            hipHostMalloc(&P.h_spec_tab, n * E * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
+            return -2;
+        P.spec_tab_cap = n * E;
+    }
+    const size_t need = n * K;
+    if (P.spec_cap >= need) return 0;
+    if (P.spec_idx_dev) (void)hipFree(P.spec_idx_dev);
+    if (P.h_spec) (void)hipHostFree(P.h_spec);
+    P.spec_idx_dev = P.h_spec = nullptr;
+    P.spec_cap = 0;
+    if (hipMalloc(&P.spec_idx_dev, need * sizeof(uint32_t)) != hipSuccess ||
+        hipHostMalloc(&P.h_spec, (1 + need) * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+        return -2;
+    P.spec_cap = need;
+    return 0;
+}
+
+// The host's side of a layer that ran in a speculative run, once its picks
+// are back: the routing-prediction scores and the last-token record, as the
+// per-layer path makes them, then the layer's gets in pick order (repeats
+// dropped).  Every pick had a slot (else the layer would have stopped the
+// run) and no fill ran since the slot maps were taken, so each get is a hit:
+// the LRU touch, the pin and the op log entry of a hit.
+int spec_account(uint32_t layer, const uint32_t *picks, uint32_t K) {
+    StreamPool &P = g.pool;
+    LayerHost &L = *find_layer(layer);
+    const auto it = P.tok_ids.find(layer);
+    if (it != P.tok_ids.end()) {
+        P.tok_stats.score(it->second, picks, K);
+        P.tok_ids.erase(it);
+    }
+    P.pred_ids.erase(layer);
+    P.last_pred.record(layer, picks, K);
+    std::vector<uint32_t> sel;
+    for (uint32_t k = 0; k < K; ++k) {
+        const uint32_t e = std::min(picks[k], L.d.experts - 1);
+        if (std::find(sel.begin(), sel.end(), e) == sel.end()) sel.push_back(e);
+    }
+    P.epoch++;
+    pool_log(kOpEpoch, layer, 0, 0);
+    for (uint32_t e : sel) {
+        P.sched.cancel(cz::ExpertKey{layer, e});
+        const auto w = P.where.find(pool_key(layer, e));
+        if (w == P.where.end()) {
+            snprintf(g_err, sizeof g_err, "layer %u ran on expert %u without a pool slot", layer, e);
+            return -5;
+        }
+        const uint32_t i = w->second;
+        P.hits++;
+        if (P.prefetched[i]) {
+            if (P.prefetched[i] == P.stats_epoch + 1) P.prefetch_hits++;
+            P.prefetched[i] = 0;
+        }
+        P.used[i] = ++P.clock;
+        P.pin_epoch[i] = P.epoch;
+        pool_log(kOpGet, layer, e, i | kLogHit);
+    }
+    return 0;
+}
+
+// The later streamed layers of a one-token chain with the host off their
+// path.  The prefetches queued so far are serviced first; then every
+// layer's slot map (every resident expert of it: no fill runs until the run
+// is over) goes to the device in one copy on the compute stream, and each
+// layer's three kernels follow, after a wait for the latest fill of any slot
+// in its map, all enqueued at once.  A layer whose routing picks an expert without a slot
+// sets the stop word and every later kernel does nothing; x is then the
+// output of the last layer that ran.  One read-back after the run; the
+// layers that ran are accounted in order.  *done: how many layers ran.
+int run_spec_layers(const std::vector<uint32_t> &layers, size_t j0, float *x, float eps, hipStream_t st,
+                    size_t *done) {
+    StreamPool &P = g.pool;
+    const size_t n = layers.size() - j0;
+    const uint32_t K = find_layer(layers[j0])->d.topk, E = find_layer(layers[j0])->d.experts;
+    *done = 0;
+    if (int rc = pool_service()) return rc;
+    if (int rc = ensure_spec(n, E, K)) return rc;
+    for (size_t j = 0; j < n; ++j)
+        memcpy(P.h_spec_tab + j * E, find_layer(layers[j0 + j])->slot_map.data(), E * sizeof(int32_t));
+    CZ_CHECK(hipMemcpyAsync(P.spec_tab_dev, P.h_spec_tab, n * E * sizeof(int32_t), hipMemcpyHostToDevice, st), -3);
+    CZ_CHECK(hipMemsetAsync(P.stop_dev, 0, sizeof(uint32_t), st), -4);
+    for (size_t j = 0; j < n; ++j) {
+        LayerHost &L = *find_layer(layers[j0 + j]);
+        std::vector<uint32_t> slots;
+        for (uint32_t e = 0; e < E; ++e)
+            if (L.slot_map[e] >= 0) slots.push_back((uint32_t)L.slot_map[e]);
+        if (int rc = wait_fills(st, slots.data(), slots.size())) return rc;
+        StepArgs A = step_args(L, x, 1, x, 1, eps, x, nullptr, P.spec_idx_dev + j * K, nullptr);
+        A.L.slot_map = P.spec_tab_dev + j * E;  // this run's map of the layer
+        A.stop = P.stop_dev;
+        A.stop_code = (uint32_t)j + 1;
+        if (int rc = launch_step(A, st)) return rc;
+    }
+    CZ_CHECK(hipMemcpyAsync(P.h_spec, P.stop_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
+    CZ_CHECK(hipMemcpyAsync(P.h_spec + 1, P.spec_idx_dev, n * K * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
+    CZ_CHECK(hipEventRecord(P.ev_idx, st), -4);
+    for (;;) {
+        const hipError_t q = hipEventQuery(P.ev_idx);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) {
+            snprintf(g_err, sizeof g_err, "speculative run read-back: %s", hipGetErrorString(q));
+            return -5;
+        }
+    }
+    const uint32_t stop = P.h_spec[0];
+    const size_t ran = stop ? std::min((size_t)stop - 1, n) : n;
+    for (size_t j = 0; j < ran; ++j)
+        if (int rc = spec_account(layers[j0 + j], P.h_spec + 1 + j * K, K)) return rc;
+    P.spec_layers += ran;
+    if (stop) P.spec_stops++;
+    *done = ran;
+    return 0;
+}
+
 }  // namespace
 
 // The pool's configured shape is fixed until colizig_hip_stream_pool_free.
@@ -2857,8 +3024,10 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
         return -2;
     if (!P.copy) {
         CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);
+        CZ_CHECK(hipStreamCreateWithFlags(&P.copy_hi, hipStreamNonBlocking), -4);
         CZ_CHECK(hipEventCreateWithFlags(&P.ev_idx, hipEventDisableTiming), -4);
         CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy, hipEventDisableTiming), -4);
+        CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy_hi, hipEventDisableTiming), -4);
     }
     P.d = d;
     P.w_slot = w_slot;
@@ -2871,7 +3040,8 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
         P.slot_ev.push_back(e);
     }
     P.fill_seq.assign(n, 0);
-    P.fill_counter = P.waited_seq = 0;
+    P.fill_sid.assign(n, 0);
+    P.fill_counter = P.waited[0] = P.waited[1] = 0;
     P.key.assign(n, 0);
     P.used.assign(n, 0);
     P.prefetched.assign(n, 0);
@@ -2893,6 +3063,7 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     if (!g.inited || !P.on) return -1;
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
     CZ_CHECK(hipStreamSynchronize(P.copy), -5);
+    CZ_CHECK(hipStreamSynchronize(P.copy_hi), -5);
     for (auto it = g.layers.begin(); it != g.layers.end();) {
         if (it->second.streamed()) {
             free_layer(it->second);
@@ -2916,7 +3087,7 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     P.next_stats = cz::PredStats{};
     P.tok_ids.clear();
     P.tok_stats = cz::PredStats{};
-    P.fill_counter = P.waited_seq = 0;
+    P.fill_counter = P.waited[0] = P.waited[1] = 0;
     P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
         P.bytes_h2d = 0;
     P.log.clear();
@@ -2934,6 +3105,7 @@ int stream_layer_setup(LayerHost *L, uint32_t layer) {
     }
     (void)hipStreamSynchronize(g.stream);
     (void)hipStreamSynchronize(P.copy);
+    (void)hipStreamSynchronize(P.copy_hi);
     if (!L->streamed()) {
         if (L->ew) (void)hipFree(L->ew);
         if (L->es) (void)hipFree(L->es);
@@ -3020,6 +3192,14 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
                                L.d.norm_topk == find_layer(later[0])->d.norm_topk)))
             later.push_back(layer0 + l);
     }
+    // speculative runs (prediction bits 1 and 2): every layer after the
+    // first is a predicted streamed one, with an f32 router and no NativeMatrix
+    // shared expert
+    bool spec = S == 1 && (P.predict_mode & 6) == 6 && first == 0 && later.size() + 1 == nlayers;
+    for (size_t j = 0; spec && j < later.size(); ++j) {
+        const LayerHost &Lj = *find_layer(later[j]);
+        spec = later[j] == layer0 + 1 + j && Lj.shn_dtype < 0 && !Lj.router_bf16;
+    }
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost &L = *find_layer(layer0 + l);
         LayerHost *next = l + 1 < nlayers ? find_layer(layer0 + l + 1) : nullptr;
@@ -3027,6 +3207,13 @@ extern "C" int colizig_hip_stream_decode(uint32_t layer0, uint32_t nlayers, floa
                                                          layer0 + l + 1, st, l == first ? &later : nullptr)
                                     : launch_layer(L, x_dev, S, x_dev, 1, eps, x_dev, nullptr, nullptr, nullptr, st);
         if (rc) return rc;
+        if (spec && l + 1 < nlayers) {
+            // the layers from l + 1 in one run; the layer that stopped it goes
+            // through the per-layer path, then the next run starts after it
+            size_t ran = 0;
+            if (int rc2 = run_spec_layers(later, l, x_dev, eps, st, &ran)) return rc2;
+            l += (uint32_t)ran;
+        }
     }
     return 0;
 }
@@ -3105,7 +3292,8 @@ extern "C" int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32
         ++warmed;
     }
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
-    P.waited_seq = P.fill_counter;  // every fill is complete
+    CZ_CHECK(hipStreamSynchronize(P.copy_hi), -3);
+    P.waited[0] = P.waited[1] = P.fill_counter;  // every fill is complete
     return (int)warmed;
 }
 
@@ -3117,13 +3305,14 @@ extern "C" int colizig_hip_stream_evict_all(void) {
     StreamPool &P = g.pool;
     if (!g.inited || !P.on) return -1;
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
+    CZ_CHECK(hipStreamSynchronize(P.copy_hi), -3);
     CZ_CHECK(hipStreamSynchronize(g.stream), -3);
     for (uint32_t i = 0; i < P.nslots; ++i) {
         P.key[i] = 0;
         P.prefetched[i] = 0;
     }
     P.where.clear();
-    P.waited_seq = P.fill_counter;  // every fill is complete
+    P.waited[0] = P.waited[1] = P.fill_counter;  // every fill is complete
     P.sched.clear();
     P.pred_ids.clear();
     P.tok_ids.clear();
@@ -3149,6 +3338,7 @@ extern "C" int colizig_hip_stream_stats_reset(void) {
         P.bytes_h2d = 0;
     P.next_stats = cz::PredStats{};
     P.tok_stats = cz::PredStats{};
+    P.spec_layers = P.spec_stops = 0;
     P.last_pred.reset_stats();
     P.sched.reset_stats();
     return 0;
@@ -3160,13 +3350,14 @@ extern "C" int colizig_hip_stream_stats(uint64_t *out, int n) {
     const StreamPool &P = g.pool;
     const cz::SchedStats &s = P.sched.stats();
     const cz::PredStats &lt = P.last_pred.stats();
-    const uint64_t v[25] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
+    const uint64_t v[27] = {P.hits, P.misses, P.loads, P.evictions, P.prefetch_issued, P.prefetch_hits,
                             P.prefetch_wasted, P.bytes_h2d, P.nslots, (uint64_t)P.where.size(),
                             P.next_stats.predicted, P.next_stats.correct, lt.predicted, lt.correct,
                             s.submitted, s.deduped, s.upgraded, s.rejected_full, s.serviced[0], s.serviced[1],
-                            s.serviced[2], s.cancelled, s.queue_peak, P.tok_stats.predicted, P.tok_stats.correct};
+                            s.serviced[2], s.cancelled, s.queue_peak, P.tok_stats.predicted, P.tok_stats.correct,
+                            P.spec_layers, P.spec_stops};
     if (!out || n < 1) return -1;
-    for (int i = 0; i < n && i < 25; ++i) out[i] = v[i];
+    for (int i = 0; i < n && i < 27; ++i) out[i] = v[i];
     return 0;
 }
 
@@ -3175,7 +3366,7 @@ extern "C" int colizig_hip_stream_stats(uint64_t *out, int n) {
 extern "C" int colizig_hip_stream_set_predict(int mode) {
     CsrGuard csr;
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (mode < 0 || mode > 3) return -1;
+    if (mode < 0 || mode > 7) return -1;
     const int prev = g.pool.predict_mode;
     g.pool.predict_mode = mode;
     return prev;

@@ -123,11 +123,24 @@ struct StepArgs {
     // and writes the picks to host_idx, then host_seq to host_flag
     uint32_t *route_count, *host_idx, *host_flag;
     uint32_t host_seq;
+    // nullable: a streamed token run with the host off the per-layer path.
+    // Every kernel of a layer exits at once while the word is nonzero; the
+    // gate/up kernel stores stop_code there when one of the token's picks
+    // has no pool slot (slot_map < 0), and then neither publishes nor counts
+    // the routing, so the layer and every later one leave x as it was.
+    uint32_t *stop;
+    uint32_t stop_code;
     int S;
     int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
     int rms;
     float eps;
 };
+
+// A streamed token's stop word is set (an earlier layer, or this one, met a
+// pick without a pool slot): the kernel does nothing.
+__device__ __forceinline__ bool cz_stopped(const StepArgs &A) {
+    return A.stop && __builtin_nontemporal_load(A.stop) != 0u;
+}
 
 // ---------------------------------------------------------------------------
 // bit-exact dequantisation (test hook): out = e4m3(w) * scale, one multiply
@@ -304,6 +317,7 @@ __device__ inline void cz_route_wave_m(const float *__restrict__ lg, uint32_t E,
 // launch.
 template <int NS>
 __global__ __launch_bounds__(64) void k_router_fast(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     constexpr uint32_t H = 32 * NS;
     const uint32_t E = A.L.E;
     const uint32_t lane = threadIdx.x & 63;
@@ -728,6 +742,7 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
 }
 
 __global__ __launch_bounds__(64) void k_router_generic(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     const uint32_t H = A.L.H, E = A.L.E;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t half = lane >> 5, j = lane & 31, hb = half * 32;
@@ -894,6 +909,17 @@ __device__ inline UpItem cz_up_item(const StepArgs &A, uint32_t rows_wg, const f
         }
         CZ_UP_STORE_X()
         __syncthreads();
+        if (A.stop && L.slot_map) {  // block-uniform: a pick without a pool slot stops the token's run
+            bool miss = false;
+            for (uint32_t k = 0; k < L.K; ++k) miss = miss || L.slot_map[s_idx[k]] < 0;
+            if (miss) {
+                if (threadIdx.x == 0) atomicCAS(A.stop, 0u, A.stop_code);
+                it.rows = 0;  // the caller's rows test ends the block
+                it.tok = 0;
+                it.tile = 0;
+                return it;
+            }
+        }
         if (z == 0 && it.tile == 0 && wave == 0) {
             for (uint32_t k = lane; k < L.K; k += 64) {
                 const uint64_t o = (uint64_t)it.tok * L.K + k;
@@ -1254,6 +1280,7 @@ __device__ inline void cz_up_rows(const StepArgs &A, const UpItem &it, const flo
 
 template <int NB, int RW, int M>
 __global__ __launch_bounds__(256) void k_up_fast(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     __shared__ float4 xs[NB * 16];  // the token's router input, H = 64*NB floats
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xn = A.rms ? A.xn : A.x;
@@ -1366,6 +1393,7 @@ __device__ inline void cz_down_row(const StepArgs &A, uint32_t tok, uint32_t r, 
 
 template <int NJ, int NJS, int KC>
 __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tiles_h = (L.H + 3) / 4;
@@ -1385,6 +1413,7 @@ __global__ __launch_bounds__(256) void k_down_fast(StepArgs A) {
 // KM = top-k (experts in pick order).
 template <int BPL, int NQ, int KM, int RR>
 __global__ __launch_bounds__(256) void k_down_rows(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     constexpr int ND = BPL / 4;
     static_assert(BPL == 4 || BPL == 8 || BPL == 12 || BPL == 16, "bytes per lane");
     const LayerDev &L = A.L;
@@ -1510,6 +1539,7 @@ __device__ inline float cz_dot_fp8_strided(const uint8_t *__restrict__ w, const 
 
 template <int M>
 __global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xn = A.rms ? A.xn : A.x;
@@ -1525,6 +1555,7 @@ __global__ __launch_bounds__(256) void k_up_generic(StepArgs A) {
 }
 
 __global__ __launch_bounds__(256) void k_down_generic(StepArgs A) {
+    if (cz_stopped(A)) return;  // block-uniform
     const LayerDev &L = A.L;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tiles_h = (L.H + 3) / 4;

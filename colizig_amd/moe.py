@@ -332,7 +332,8 @@ STREAM_STAT_NAMES = ("hits", "misses", "loads", "evictions", "prefetch_issued", 
                      "prefetch_wasted", "bytes_h2d", "slots", "resident", "next_predicted", "next_correct",
                      "last_predicted", "last_correct", "sched_submitted", "sched_deduped", "sched_upgraded",
                      "sched_rejected_full", "sched_serviced_high", "sched_serviced_medium", "sched_serviced_low",
-                     "sched_cancelled", "sched_queue_peak", "tok_predicted", "tok_correct")
+                     "sched_cancelled", "sched_queue_peak", "tok_predicted", "tok_correct", "spec_layers",
+                     "spec_stops")
 
 
 def stream_pool_init(d: Dims, cap_bytes: int) -> None:

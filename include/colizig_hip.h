@@ -353,13 +353,14 @@ int colizig_hip_stream_usage(uint32_t layer0, uint32_t nlayers, uint32_t experts
 int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32_t experts, const uint64_t *counts);
 int colizig_hip_stream_evict_all(void);
 
-/* Pool counters, out[0..n) (n <= 25): hits, misses, loads, evictions,
+/* Pool counters, out[0..n) (n <= 27): hits, misses, loads, evictions,
  * prefetch_issued, prefetch_hits, prefetch_wasted (CacheStats,
  * moe.zig:121-139), bytes_h2d, slots, resident entries; next-layer
  * prediction: ids predicted, ids correct; last-token prediction: predicted,
  * correct (predict.zig:19-27); scheduler (io.zig:38-52): submitted, deduped,
  * upgraded, rejected_full, serviced HIGH / MEDIUM / LOW, cancelled,
- * queue_peak; token-level prediction: predicted, correct. */
+ * queue_peak; token-level prediction: predicted, correct; layers run in
+ * speculative runs, runs stopped by a pick without a slot. */
 int colizig_hip_stream_stats(uint64_t *out, int n);
 /* Opens a new statistics window: every counter above restarts at 0 (the
  * scheduler's queue peak at the queue's current length), and a prefetch
@@ -372,8 +373,16 @@ int colizig_hip_stream_stats_reset(void);
  * layer's routing from the current layer's router input (its router and
  * routing kernels run once more on that input); bit 1, every later streamed
  * layer's from the chain's first streamed layer's router input (one router
- * launch over those layers, one routing launch).  Default 2.  Returns the
- * previous mode, -1 for a mode outside 0..3. */
+ * launch over those layers, one routing launch).  Bit 2 (with bit 1, every
+ * layer after the first streamed, f32 routers): the host leaves the
+ * per-layer path.  After the first layer's prediction is serviced, every
+ * later layer's slot map (all its resident experts) and its three kernels
+ * are enqueued at once.  A layer that picks an expert without a slot stops
+ * the rest of the run through a device word; that layer goes through the
+ * per-layer path, and a new run starts after it.  The layers that ran are
+ * then accounted in order (LRU touches, op log, counters, prediction
+ * scores), as the per-layer path does.  Default 6.  Returns the previous
+ * mode, -1 for a mode outside 0..7. */
 int colizig_hip_stream_set_predict(int mode);
 
 /* Op log of the pool's policy (test hook).  colizig_hip_stream_log(1) clears

@@ -3,8 +3,11 @@
 pinned host memory (packed slabs, one copy per fill), an HBM pool of 64
 slots (the working set is 512 experts), routing Zipf(1.2)-skewed over a
 seeded permutation per layer with 10% of the experts swapping ranks after
-every step, 32 decode steps at batch 1 with both routing predictions on
-(next layer, and every later layer from the token's first router input).
+every step, 32 decode steps at batch 1.  Two routing-prediction modes:
+both predictions (next layer, and every later layer from the token's first
+router input), and the token-level one with the later layers run with the
+host off their path (speculative runs: a pick without a slot stops the run,
+that layer goes through the per-layer path, and a new run follows).
 
 Against the oracle:
 - every layer's demand gets (its picks, in pick order, repeats dropped)
@@ -61,8 +64,8 @@ def host_layer(L: moe.Layer, d: moe.Dims, bias: np.ndarray):
     return host, packed
 
 
-@pytest.fixture(scope="module")
-def c5(gpu, oracle_lib):
+@pytest.fixture(scope="module", params=[3, 6], ids=["predict3", "predict6_speculative"])
+def c5(gpu, oracle_lib, request):
     d = moe.dims(H, E, K, I)
     moe.stream_pool_init(d, NSLOTS * moe.packed_expert_bytes(d))
     assert moe.stream_stats()["slots"] == NSLOTS
@@ -81,8 +84,8 @@ def c5(gpu, oracle_lib):
         hosts.append(host)
         packs.append(packed)
         layers.append(L)
-    prev = hip.colizig_hip_stream_set_predict(3)  # both predictions: the op log covers both kinds of prefetch
-    yield dict(d=d, hosts=hosts, packs=packs, layers=layers, ranks=ranks, rng=rng)
+    prev = hip.colizig_hip_stream_set_predict(request.param)
+    yield dict(d=d, hosts=hosts, packs=packs, layers=layers, ranks=ranks, rng=rng, mode=request.param)
     hip.colizig_hip_stream_set_predict(prev)
     hip.colizig_hip_stream_log(0)
     moe.stream_pool_free()
@@ -91,7 +94,8 @@ def c5(gpu, oracle_lib):
 
 
 def test_c5_stream_vs_oracle_chain_and_policy(c5, oracle_lib):
-    say("c5: 4 streamed layers, 64-slot pool, Zipf(1.2) with 10% drift, 32 steps")
+    mode = c5["mode"]
+    say(f"c5: 4 streamed layers, 64-slot pool, Zipf(1.2) with 10% drift, 32 steps, prediction mode {mode}")
     hip = _lib.hip()
     orcs = [oracle_lib.OracleLayer(h) for h in c5["hosts"]]
     rng, ranks = c5["rng"], c5["ranks"]
@@ -146,9 +150,16 @@ def test_c5_stream_vs_oracle_chain_and_policy(c5, oracle_lib):
         assert lib_st[k] == v, (k, lib_st[k], v)
     assert lib_st["resident"] == r
     assert lib_st["hits"] + lib_st["misses"] == sum(len(s) for _, s in picks_o)
-    assert lib_st["next_predicted"] == (STEPS * NL - STEPS) * K  # every layer but the first of each step
+    # every layer but the first of each step
+    assert lib_st["next_predicted"] == ((STEPS * NL - STEPS) * K if mode & 1 else 0)
     assert lib_st["tok_predicted"] == (STEPS * NL - STEPS) * K
-    acc = lib_st["next_correct"] / lib_st["next_predicted"]
+    if mode & 4:  # speculative runs ran layers, and missing slots stopped some (their layers re-ran above)
+        assert lib_st["spec_layers"] > 0 and lib_st["spec_stops"] > 0, lib_st
+        assert lib_st["spec_layers"] + lib_st["spec_stops"] <= STEPS * (NL - 1)
+        say(f"  speculative: {lib_st['spec_layers']} layers ran, {lib_st['spec_stops']} runs stopped")
+    else:
+        assert lib_st["spec_layers"] == 0
+    acc = lib_st["next_correct"] / max(lib_st["next_predicted"], 1)
     say(f"  x rel L2 <= {worst:.2e}; {len(ops)} pool ops replayed; hits {lib_st['hits']} misses "
         f"{lib_st['misses']} evictions {lib_st['evictions']}; prefetch issued {lib_st['prefetch_issued']} hits "
         f"{lib_st['prefetch_hits']} wasted {lib_st['prefetch_wasted']}; next-layer prediction {acc:.3f}")
