@@ -504,11 +504,11 @@ void launch_router(const StepArgs &A, hipStream_t st) {
         const uint32_t ge = (L.E + CZ_RT_EXP - 1) / CZ_RT_EXP;
         const uint32_t S = (uint32_t)A.S;
         if (ge * ((S + 15) / 16) >= 256)
-            k_router_tiled<16><<<dim3(ge, (S + 15) / 16), 256 * CZ_RT_TG, 0, st>>>(A);
+            k_router_tiled<16><<<dim3((S + 15) / 16, ge), 256 * CZ_RT_TG, 0, st>>>(A);
         else if (ge * ((S + 7) / 8) >= 256)
-            k_router_tiled<8><<<dim3(ge, (S + 7) / 8), 256 * CZ_RT_TG, 0, st>>>(A);
+            k_router_tiled<8><<<dim3((S + 7) / 8, ge), 256 * CZ_RT_TG, 0, st>>>(A);
         else
-            k_router_tiled<4><<<dim3(ge, (S + 3) / 4), 256 * CZ_RT_TG, 0, st>>>(A);
+            k_router_tiled<4><<<dim3((S + 3) / 4, ge), 256 * CZ_RT_TG, 0, st>>>(A);
         return;
     }
     const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);

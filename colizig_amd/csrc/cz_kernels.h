@@ -648,8 +648,11 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
     const LayerDev &L = A.L;
     const uint32_t H = L.H, E = L.E;
     const uint32_t tid = threadIdx.x, col = tid & 255, g = tid >> 8, hw = col >> 5, j = col & 31;
-    const uint32_t ea = min(blockIdx.x * CZ_RT_EXP + 2 * hw, E - 1), eb = min(blockIdx.x * CZ_RT_EXP + 2 * hw + 1, E - 1);
-    const uint32_t t0 = blockIdx.y * TOK;
+    // grid (token tiles, expert groups): block b runs on XCD b % 8, so each
+    // XCD takes every eighth token tile with all the expert groups, and its
+    // L2 fetches its tokens' rows and the router once
+    const uint32_t ea = min(blockIdx.y * CZ_RT_EXP + 2 * hw, E - 1), eb = min(blockIdx.y * CZ_RT_EXP + 2 * hw + 1, E - 1);
+    const uint32_t t0 = blockIdx.x * TOK;
     const uint32_t nt = min((uint32_t)TOK, (uint32_t)A.S - t0);
     constexpr uint32_t XBUF = 2 * TOK * 256, ACCN = CZ_RT_EXP * TOK * CZ_RT_ACC_LD;
     __shared__ __align__(16) float s_buf[XBUF > ACCN ? XBUF : ACCN];
@@ -733,7 +736,7 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
         total = total + a[l + 24];
         sum = sum + total;
     }
-    const uint32_t e = blockIdx.x * CZ_RT_EXP + el;
+    const uint32_t e = blockIdx.y * CZ_RT_EXP + el;
     if (e < E && t < nt) {
         float lg = sum;
         if (L.router_bias) lg = lg + L.router_bias[e];
