@@ -503,12 +503,20 @@ void launch_router(const StepArgs &A, hipStream_t st) {
         // tokens per workgroup: the most that still gives 256 workgroups
         const uint32_t ge = (L.E + CZ_RT_EXP - 1) / CZ_RT_EXP;
         const uint32_t S = (uint32_t)A.S;
+        auto launch = [&](auto TOKc) {
+            constexpr int TOK = decltype(TOKc)::value;
+            const uint32_t tiles = (S + TOK - 1) / TOK;
+            if (S > L.E)  // more input rows than router rows: token tiles across the XCDs
+                k_router_tiled<TOK, true><<<dim3(tiles, ge), 256 * CZ_RT_TG, 0, st>>>(A);
+            else
+                k_router_tiled<TOK, false><<<dim3(ge, tiles), 256 * CZ_RT_TG, 0, st>>>(A);
+        };
         if (ge * ((S + 15) / 16) >= 256)
-            k_router_tiled<16><<<dim3((S + 15) / 16, ge), 256 * CZ_RT_TG, 0, st>>>(A);
+            launch(std::integral_constant<int, 16>{});
         else if (ge * ((S + 7) / 8) >= 256)
-            k_router_tiled<8><<<dim3((S + 7) / 8, ge), 256 * CZ_RT_TG, 0, st>>>(A);
+            launch(std::integral_constant<int, 8>{});
         else
-            k_router_tiled<4><<<dim3((S + 3) / 4, ge), 256 * CZ_RT_TG, 0, st>>>(A);
+            launch(std::integral_constant<int, 4>{});
         return;
     }
     const dim3 grid((L.E + 1) / 2, (A.S + A.tt - 1) / A.tt);

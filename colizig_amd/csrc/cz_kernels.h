@@ -642,17 +642,20 @@ __global__ __launch_bounds__(256) void k_rms_rows(StepArgs A) {
 #define CZ_RT_ACC_LD 36  // floats per (expert, token) row of chain sums (16 B aligned, b128 conflict-free)
 #define CZ_RT_RING 4     // register sets of chunk operands in flight
 
-template <int TOK>
+template <int TOK, bool TM>
 __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
     constexpr uint32_t NTT = TOK / CZ_RT_TG;  // tokens per thread
     const LayerDev &L = A.L;
     const uint32_t H = L.H, E = L.E;
     const uint32_t tid = threadIdx.x, col = tid & 255, g = tid >> 8, hw = col >> 5, j = col & 31;
-    // grid (token tiles, expert groups): block b runs on XCD b % 8, so each
-    // XCD takes every eighth token tile with all the expert groups, and its
-    // L2 fetches its tokens' rows and the router once
-    const uint32_t ea = min(blockIdx.y * CZ_RT_EXP + 2 * hw, E - 1), eb = min(blockIdx.y * CZ_RT_EXP + 2 * hw + 1, E - 1);
-    const uint32_t t0 = blockIdx.x * TOK;
+    // block b runs on XCD b % 8.  TM (more tokens than experts): grid (token
+    // tiles, expert groups), so each XCD takes every eighth token tile with
+    // all the expert groups and its L2 fetches its tokens' rows and the
+    // router once; else grid (expert groups, token tiles), so each XCD's L2
+    // fetches an eighth of the router and all the rows
+    const uint32_t eg = TM ? blockIdx.y : blockIdx.x, tg = TM ? blockIdx.x : blockIdx.y;
+    const uint32_t ea = min(eg * CZ_RT_EXP + 2 * hw, E - 1), eb = min(eg * CZ_RT_EXP + 2 * hw + 1, E - 1);
+    const uint32_t t0 = tg * TOK;
     const uint32_t nt = min((uint32_t)TOK, (uint32_t)A.S - t0);
     constexpr uint32_t XBUF = 2 * TOK * 256, ACCN = CZ_RT_EXP * TOK * CZ_RT_ACC_LD;
     __shared__ __align__(16) float s_buf[XBUF > ACCN ? XBUF : ACCN];
@@ -736,7 +739,7 @@ __global__ __launch_bounds__(256 * CZ_RT_TG) void k_router_tiled(StepArgs A) {
         total = total + a[l + 24];
         sum = sum + total;
     }
-    const uint32_t e = blockIdx.y * CZ_RT_EXP + el;
+    const uint32_t e = eg * CZ_RT_EXP + el;
     if (e < E && t < nt) {
         float lg = sum;
         if (L.router_bias) lg = lg + L.router_bias[e];
