@@ -629,8 +629,24 @@ def stream_bench(args) -> None:
                 assert hip.colizig_hip_sync() == 0
                 a, b = xb.download(np.empty_like(x0)), xr.download(np.empty_like(x0))
                 same = same and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
-            parity = {"reference": f"the same {NL} layers resident (three-kernel decode) from the same x",
-                      "tokens": ntok, "bit_identical": same}
+            # as timed: the speculative runs on the one-launch decode, the
+            # resident chain on it too; the residual differs only in the
+            # order of the per-XCD partial sums (a changed pick would show
+            # as a difference of order 1e-2)
+            hip.colizig_hip_set_fused_decode(prev_fd)
+            xr.upload(xb.download(np.empty_like(x0)))
+            worst = 0.0
+            for _ in range(ntok):
+                if hip.colizig_hip_stream_decode(0, NL, xb.ptr, 1, eps) != 0 or \
+                        hip.colizig_hip_chain_decode(NL, NL, xr.ptr, 1, eps, None, None, None, None) != 0:
+                    raise RuntimeError(f"parity pass failed: {_lib.last_error()}")
+                assert hip.colizig_hip_sync() == 0
+                a, b = xb.download(np.empty_like(x0)), xr.download(np.empty_like(x0))
+                worst = max(worst, float(np.linalg.norm((a - b).astype(np.float64)) /
+                                         np.linalg.norm(b.astype(np.float64))))
+            parity = {"reference": f"the same {NL} layers resident from the same x",
+                      "tokens": ntok, "bit_identical_three_kernel": same,
+                      "one_launch_rel_l2": worst, "one_launch_ok": worst < 1e-5}
             xr.free()
         finally:
             hip.colizig_hip_set_fused_decode(prev_fd)

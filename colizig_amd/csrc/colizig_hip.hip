@@ -231,6 +231,7 @@ struct FusedState {
     uint32_t *pred = nullptr;        // [2][64] predicted experts of the next layer, ping-pong
     unsigned long long *lgpx = nullptr;  // [E] tagged next-layer logits
     unsigned long long *pstat = nullptr;  // [2] slots predicted, predictions picked
+    unsigned long long *spec_pstat = nullptr;  // [2] the same for the streaming tier's speculative runs
     int predict = 1;                 // colizig_hip_set_fused_predict
     uint32_t *run = nullptr;         // chain-run counter
     uint32_t *err_host = nullptr;    // host-coherent error word
@@ -902,9 +903,11 @@ LayerHost *find_layer(uint32_t layer);
 // The one-launch decode serves batch 1 on a device of 8 XCDs x 32 CUs for
 // resident layers without a shared expert with H in {512, 1024, 2048},
 // E <= 128, K <= 32, I a multiple of 128 and K*I/1024 in {1, 2, 4, 6, 8}.
-bool fused_ok(const LayerHost &L, int S) {
+// The one-launch decode's shape and device conditions; a streamed layer
+// runs it only inside a speculative run (slot maps on the device).
+bool fused_shape_ok(const LayerHost &L, int S) {
     const colizig_dims &d = L.d;
-    if (!g.fused.enabled || S != 1 || L.streamed() || g.fused.cus != CZ_FWG || !g.fused.placement_ok) return false;
+    if (!g.fused.enabled || S != 1 || g.fused.cus != CZ_FWG || !g.fused.placement_ok) return false;
     if (d.shared_inter != 0 || d.experts > 128 || d.topk > 32 || d.inter % CZ_BLOCK || L.router_bf16)
         return false;
     if (d.hidden != 512 && d.hidden != 1024 && d.hidden != 2048) return false;
@@ -914,13 +917,16 @@ bool fused_ok(const LayerHost &L, int S) {
     return rw == 1 || rw == 2 || rw == 4 || rw == 6 || rw == 8;
 }
 
+bool fused_ok(const LayerHost &L, int S) { return !L.streamed() && fused_shape_ok(L, S); }
+
 int ensure_fused(const colizig_dims &d) {
     FusedState &F = g.fused;
     const size_t ki = (size_t)d.topk * d.inter;
     if (!F.run) {
         if (hipMalloc(&F.run, 256) != hipSuccess) return -2;
         if (hipMemset(F.run, 0, 256) != hipSuccess) return -2;
-        F.pstat = reinterpret_cast<unsigned long long *>(F.run) + 16;  // bytes 128..143 of the same block
+        F.pstat = reinterpret_cast<unsigned long long *>(F.run) + 16;       // bytes 128..143 of the same block
+        F.spec_pstat = reinterpret_cast<unsigned long long *>(F.run) + 18;  // bytes 144..159
         if (hipMalloc(&F.pred, 2 * 64 * sizeof(uint32_t)) != hipSuccess) return -2;
         if (hipMemset(F.pred, 0, 2 * 64 * sizeof(uint32_t)) != hipSuccess) return -2;
         if (hipHostMalloc(&F.err_host, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) return -2;
@@ -960,23 +966,27 @@ int ensure_fused(const colizig_dims &d) {
     return 0;
 }
 
-template <int NB, bool SPEC>
+template <int NB, bool SPEC, bool STOP>
 void launch_fused_spec(const FusedArgs &A, uint32_t rw, hipStream_t st) {
     switch (rw) {
-        case 1: k_layer_fused<NB, 1, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
-        case 2: k_layer_fused<NB, 2, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
-        case 4: k_layer_fused<NB, 4, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
-        case 6: k_layer_fused<NB, 6, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
-        default: k_layer_fused<NB, 8, SPEC><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 1: k_layer_fused<NB, 1, SPEC, STOP><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 2: k_layer_fused<NB, 2, SPEC, STOP><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 4: k_layer_fused<NB, 4, SPEC, STOP><<<CZ_FWG, 512, 0, st>>>(A); return;
+        case 6: k_layer_fused<NB, 6, SPEC, STOP><<<CZ_FWG, 512, 0, st>>>(A); return;
+        default: k_layer_fused<NB, 8, SPEC, STOP><<<CZ_FWG, 512, 0, st>>>(A); return;
     }
 }
 
+// A speculative run's layers (A.stop set, with their slot maps and the
+// token-level prediction) take the kernels built with STOP.
 template <int NB>
 void launch_fused_nb(const FusedArgs &A, uint32_t rw, hipStream_t st) {
-    if (A.pred_in)
-        launch_fused_spec<NB, true>(A, rw, st);
+    if (A.stop && A.pred_in && A.L.slot_map)
+        launch_fused_spec<NB, true, true>(A, rw, st);
+    else if (A.pred_in)
+        launch_fused_spec<NB, true, false>(A, rw, st);
     else
-        launch_fused_spec<NB, false>(A, rw, st);
+        launch_fused_spec<NB, false, false>(A, rw, st);
 }
 
 // The layers [layer0, layer0 + n) (all fused_ok, one hidden size) as n
@@ -2958,17 +2968,68 @@ int run_spec_layers(const std::vector<uint32_t> &layers, size_t j0, float *x, fl
         memcpy(P.h_spec_tab + j * E, find_layer(layers[j0 + j])->slot_map.data(), E * sizeof(int32_t));
     CZ_CHECK(hipMemcpyAsync(P.spec_tab_dev, P.h_spec_tab, n * E * sizeof(int32_t), hipMemcpyHostToDevice, st), -3);
     CZ_CHECK(hipMemsetAsync(P.stop_dev, 0, sizeof(uint32_t), st), -4);
+    // the one-launch decode where every layer of the run has its shape: one
+    // launch per layer, its predicted experts the token-level prediction
+    // (k_layer_fused with slot maps and the stop word), then k_spec_final
+    const LayerHost &F0 = *find_layer(layers[j0]);
+    const uint32_t H = F0.d.hidden;
+    bool fused = P.tok_idx != nullptr && P.tok_cap >= layers.size() && n < 1023;
+    for (size_t j = 0; fused && j < n; ++j) {
+        const LayerHost &L = *find_layer(layers[j0 + j]);
+        fused = fused_shape_ok(L, 1) && L.d.hidden == H && L.d.experts == E && L.d.topk == K;
+    }
+    for (size_t j = 0; fused && j < n; ++j)
+        if (int rc = ensure_fused(find_layer(layers[j0 + j])->d)) return rc;
+    FusedState &F = g.fused;
     for (size_t j = 0; j < n; ++j) {
         LayerHost &L = *find_layer(layers[j0 + j]);
         std::vector<uint32_t> slots;
         for (uint32_t e = 0; e < E; ++e)
             if (L.slot_map[e] >= 0) slots.push_back((uint32_t)L.slot_map[e]);
         if (int rc = wait_fills(st, slots.data(), slots.size())) return rc;
-        StepArgs A = step_args(L, x, 1, x, 1, eps, x, nullptr, P.spec_idx_dev + j * K, nullptr);
-        A.L.slot_map = P.spec_tab_dev + j * E;  // this run's map of the layer
-        A.stop = P.stop_dev;
-        A.stop_code = (uint32_t)j + 1;
-        if (int rc = launch_step(A, st)) return rc;
+        if (fused) {
+            FusedArgs A{};
+            A.L = L.dev();
+            A.L.slot_map = P.spec_tab_dev + j * E;  // this run's map of the layer
+            A.rin = j <= 1 ? x : F.r + (uint64_t)((j - 1) % 2) * H;
+            A.pin = j == 0 ? F.zero : F.p + (uint64_t)((j - 1) % 2) * CZ_NXCD * H;
+            A.has_pin = j == 0 ? 0u : 1u;
+            A.rout = j == 0 ? nullptr : F.r + (uint64_t)(j % 2) * H;
+            A.pout = F.p + (uint64_t)(j % 2) * CZ_NXCD * H;
+            A.lgx = F.lgx;
+            A.hx = F.hx;
+            A.run = F.run;
+            A.err = F.err_dev;
+            A.idx_trace = P.spec_idx_dev + j * K;
+            A.pos = (uint32_t)j;
+            A.eps = eps;
+            A.pred_in = P.tok_idx + (j0 + j) * K;  // the token-level prediction of this layer
+            A.lgpx = F.lgpx;
+            A.pstat = F.spec_pstat;
+            A.poll_mask = ~0u;
+            A.stop = P.stop_dev;
+            A.stop_code = (uint32_t)j + 1;
+            const uint32_t rw = (uint32_t)((uint64_t)K * L.d.inter / 1024);
+            switch (H) {
+                case 512: launch_fused_nb<8>(A, rw, st); break;
+                case 1024: launch_fused_nb<16>(A, rw, st); break;
+                default: launch_fused_nb<32>(A, rw, st); break;
+            }
+        } else {
+            StepArgs A = step_args(L, x, 1, x, 1, eps, x, nullptr, P.spec_idx_dev + j * K, nullptr);
+            A.L.slot_map = P.spec_tab_dev + j * E;  // this run's map of the layer
+            A.stop = P.stop_dev;
+            A.stop_code = (uint32_t)j + 1;
+            if (int rc = launch_step(A, st)) return rc;
+        }
+    }
+    if (fused) {
+        k_spec_final<<<(H + 255) / 256, 256, 0, st>>>(x, F.r, F.p, H, (uint32_t)n, P.stop_dev, F.run);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            snprintf(g_err, sizeof g_err, "speculative run launch: %s", hipGetErrorString(e));
+            return -4;
+        }
     }
     CZ_CHECK(hipMemcpyAsync(P.h_spec, P.stop_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
     CZ_CHECK(hipMemcpyAsync(P.h_spec + 1, P.spec_idx_dev, n * K * sizeof(uint32_t), hipMemcpyDeviceToHost, st), -5);
@@ -3097,7 +3158,7 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     P.tok_stats = cz::PredStats{};
     P.fill_counter = P.waited[0] = P.waited[1] = 0;
     P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
-        P.bytes_h2d = 0;
+        P.bytes_h2d = P.spec_layers = P.spec_stops = 0;
     P.log.clear();
     return 0;
 }

@@ -78,6 +78,8 @@ struct FusedArgs {
     unsigned long long *pstat;    // [2] slots predicted, slots whose prediction was picked
     uint32_t poll_mask;           // ~0u; test hook: ~1023u makes this layer's polls wait for a tag
                                   // no layer writes (a written tag's low 10 bits are never 0)
+    uint32_t *stop;               // nullable: a speculative run's stop word (streamed layers, slot maps)
+    uint32_t stop_code;           // this layer's code in it (run position + 1)
 };
 
 typedef float cz_f4 __attribute__((ext_vector_type(4)));
@@ -207,7 +209,9 @@ __device__ inline uint32_t cz_topk_wave(const float (&lg)[2], uint32_t E, uint32
 // every slot loads after the routing.  XCD 0's control waves predict the next
 // layer's experts (its router rows on this layer's router input) once their
 // routing is done, off the weight waves' path.
-template <int NB, int RW, bool SPEC>
+// STOP: a speculative run of streamed layers (A.stop and slot maps set); the
+// resident chain's kernels are built without it.
+template <int NB, int RW, bool SPEC, bool STOP = false>
 __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     constexpr uint32_t H = 64 * NB, H4 = H / 4;
     constexpr uint32_t QX = (H4 + 255) / 256;                    // float4 of a row per thread
@@ -229,6 +233,14 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     const uint32_t NBI = I / CZ_BLOCK;                           // 128-row blocks of a slot
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    // a speculative run that an earlier layer stopped: nothing to do (the
+    // word was written before this launch, so every workgroup reads the same
+    // value; this layer's own code, stored by one of its workgroups while a
+    // late one starts, does not count)
+    if constexpr (STOP) {
+        const uint32_t sw = __builtin_nontemporal_load(A.stop);
+        if (sw != 0u && sw < A.stop_code) return;  // grid-uniform
+    }
 
     // xn, and xn and the router rows chain-major for the dotF32 chains: chain
     // j (elements j + 32 i, i < H/32) is one row of RS floats (RS = H/32 + 4
@@ -381,6 +393,20 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         uint32_t o_pos = 0, o_id = 0;
         float o_gate = 0.0f;
         cz_route_wave_regs<2>(lg, E, K, L.norm_topk, s_idx, s_gate, o_pos, o_id, o_gate);
+        // a speculative run: a pick with no pool slot stops the run here,
+        // before the routing is counted or published.  Every workgroup routes
+        // the same logits, so every one of them stops; the weight waves see
+        // stage 3 and end too.
+        if constexpr (STOP) {
+            const bool miss = lane < K && L.slot_map[o_id] < 0;
+            if (__builtin_amdgcn_ballot_w64(miss) != 0) {  // wave-uniform
+                if (lane == 0) {
+                    if (blockIdx.x == 0) atomicCAS(A.stop, 0u, A.stop_code);
+                    __hip_atomic_store(&s_stage, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                return;
+            }
+        }
         if (blockIdx.x == 0 && lane < K) cz_bump_usage(L.usage, E, o_id);
         // each slot keeps its predicted expert if it was picked (each pick
         // matched once, slots in order: the n-th slot predicting e takes the
@@ -537,6 +563,8 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         for (int i = 0; i < RW; ++i) load_down(i);
     }
     cz_lds_wait(&s_stage, 2u, A.err);  // the slots' experts and the gates are known
+    if constexpr (STOP)
+        if (__hip_atomic_load(&s_stage, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 3u) return;  // the run stopped
     routed = true;
     // gated product of row r: h = g_z * silu(Wg x) * (Wu x), to its place in block r
     auto gated_products = [&]() __attribute__((always_inline)) {
@@ -694,6 +722,30 @@ __global__ __launch_bounds__(64) void k_xcd_census(uint32_t *xcc_of) {
     uint32_t xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
     if (threadIdx.x == 0) xcc_of[blockIdx.x] = xcc & 0xffu;
+}
+
+// After a speculative run of n streamed layers: x becomes the output of the
+// last layer that ran.  Without a stop that is k_chain_final's sum over the
+// last layer's parts; when layer j stopped (stop word j + 1) it is layer j's
+// input, which its workgroup 0 kept in r[j % 2] (j >= 1), or x itself (j =
+// 0).  Advances the run counter.
+__global__ __launch_bounds__(256) void k_spec_final(float *__restrict__ x, const float *__restrict__ r,
+                                                    const float *__restrict__ p, uint32_t H, uint32_t n,
+                                                    const uint32_t *stop, uint32_t *run) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t s = *stop;
+    if (i < H) {
+        if (s == 0u) {
+            const float *rin = n == 1 ? x : r + (uint64_t)((n - 1) % 2) * H;
+            const float *pin = p + (uint64_t)((n - 1) % 2) * CZ_NXCD * H;
+            float o = pin[i];
+            for (uint32_t k = 1; k < CZ_NXCD; ++k) o = o + pin[(uint64_t)k * H + i];
+            x[i] = rin[i] + o;
+        } else if (s >= 2u) {
+            x[i] = r[(uint64_t)((s - 1u) % 2u) * H + i];
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *run = *run + 1u;
 }
 
 // After the last layer: x = residual + (((p0 + p1) + ...) + p7); advances the
