@@ -146,6 +146,7 @@ struct Work {
 // keys, a side stream for the host->HBM fills.  ExpertCache (moe.zig:121-249)
 // redesigned for one pool shared by every streamed layer.
 constexpr size_t kSchedCapacity = 64;  // queued prefetches at most (io.zig:62-63 bounded queue)
+constexpr int kCopyStreams = 3;        // copy (prefetch), copy_hi (demand), copy2 (prefetch)
 
 struct StreamPool {
     bool on = false;
@@ -163,7 +164,7 @@ struct StreamPool {
     uint64_t clock = 0;
     uint32_t epoch = 0;
     hipStream_t copy = nullptr;
-    hipEvent_t ev_idx = nullptr, ev_copy = nullptr, ev_copy_hi = nullptr;
+    hipEvent_t ev_idx = nullptr, ev_copy = nullptr, ev_copy_hi = nullptr, ev_copy2 = nullptr;
     uint32_t *h_idx = nullptr;         // pinned routing read-back (host-coherent)
     size_t h_idx_cap = 0;
     uint32_t *h_flag = nullptr;        // host-coherent: sequence number of the last one-token routing written
@@ -190,17 +191,24 @@ struct StreamPool {
     uint32_t tseq = 0;
     std::unordered_map<uint32_t, std::vector<uint32_t>> tok_ids;   // layer -> its token-level prediction
     cz::PredStats tok_stats;
-    // Fills go on two copy streams: prefetches on copy, demand fills (a
-    // layer's misses) on copy_hi, so a miss does not queue behind the
+    // Fills go on three copy streams: prefetches alternate between copy and
+    // copy2 (a fill starts while the one before it on the other stream
+    // finishes, so the link does not idle between fills), demand fills (a
+    // layer's misses) go on copy_hi, so a miss does not queue behind the
     // prefetches.  Per slot: the event recorded after its latest fill, that
     // fill's sequence number and its stream.  The compute stream has waited
     // for every fill of copy stream s up to waited[s] (each stream is in
     // order).
-    hipStream_t copy_hi = nullptr;
+    hipStream_t copy_hi = nullptr, copy2 = nullptr;
     std::vector<hipEvent_t> slot_ev;
     std::vector<uint64_t> fill_seq;
     std::vector<uint8_t> fill_sid;
-    uint64_t fill_counter = 0, waited[2] = {0, 0};
+    uint64_t fill_counter = 0, waited[kCopyStreams] = {0, 0, 0};
+    uint32_t prefetch_rr = 0;  // the stream of the next prefetch fill
+    hipStream_t copy_stream(uint8_t sid) const { return sid == 1 ? copy_hi : sid == 2 ? copy2 : copy; }
+    void all_waited() {
+        for (uint64_t &w : waited) w = fill_counter;
+    }
     cz::LastTokenPredictor last_pred{8};
     cz::Scheduler sched{kSchedCapacity};
     bool log_on = false;
@@ -1247,6 +1255,7 @@ extern "C" void colizig_cuda_shutdown(void) {
     StreamPool &P = g.pool;
     if (P.copy) (void)hipStreamSynchronize(P.copy);
     if (P.copy_hi) (void)hipStreamSynchronize(P.copy_hi);
+    if (P.copy2) (void)hipStreamSynchronize(P.copy2);
     for (void *p : {(void *)P.base, (void *)P.pred_logits, (void *)P.pred_gates, (void *)P.pred_sgate,
                     (void *)P.pred_idx, (void *)P.pred_tord, (void *)P.route_count, (void *)P.tok_logits, (void *)P.tok_gates,
                     (void *)P.tok_idx, (void *)P.tok_tord, (void *)P.tok_ptr_dev, (void *)P.stop_dev,
@@ -1259,8 +1268,10 @@ extern "C" void colizig_cuda_shutdown(void) {
     if (P.ev_idx) (void)hipEventDestroy(P.ev_idx);
     if (P.ev_copy) (void)hipEventDestroy(P.ev_copy);
     if (P.ev_copy_hi) (void)hipEventDestroy(P.ev_copy_hi);
+    if (P.ev_copy2) (void)hipEventDestroy(P.ev_copy2);
     if (P.copy) (void)hipStreamDestroy(P.copy);
     if (P.copy_hi) (void)hipStreamDestroy(P.copy_hi);
+    if (P.copy2) (void)hipStreamDestroy(P.copy2);
     (void)hipStreamDestroy(g.stream);
     g.~Ctx();
     new (&g) Ctx();
@@ -2445,9 +2456,9 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
         if (P.prefetched[i] == P.stats_epoch + 1) P.prefetch_wasted++;  // issued in this stats window
     }
     uint8_t *dst = slot_w(i);
-    const uint8_t sid = prefetch ? 0 : 1;
-    hipStream_t cs = sid ? P.copy_hi : P.copy;
-    // the slot's previous fill went through the other copy stream: this one
+    const uint8_t sid = prefetch ? ((P.prefetch_rr++ & 1u) ? 2 : 0) : 1;
+    hipStream_t cs = P.copy_stream(sid);
+    // the slot's previous fill went through another copy stream: this one
     // waits for it, so two copies never overlap in one slot
     if (P.fill_seq[i] && P.fill_sid[i] != sid && P.fill_seq[i] > P.waited[P.fill_sid[i]])
         CZ_CHECK(hipStreamWaitEvent(cs, P.slot_ev[i], 0), -4);
@@ -2483,8 +2494,8 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
 // Stream st waits for the latest fill of each copy stream among `slots`.
 int wait_fills(hipStream_t st, const uint32_t *slots, size_t n) {
     StreamPool &P = g.pool;
-    uint64_t need[2] = {P.waited[0], P.waited[1]};
-    uint32_t at[2] = {0, 0};
+    uint64_t need[kCopyStreams] = {P.waited[0], P.waited[1], P.waited[2]};
+    uint32_t at[kCopyStreams] = {0, 0, 0};
     for (size_t k = 0; k < n; ++k) {
         const uint32_t i = slots[k];
         const uint8_t s = P.fill_sid[i];
@@ -2493,7 +2504,7 @@ int wait_fills(hipStream_t st, const uint32_t *slots, size_t n) {
             at[s] = i;
         }
     }
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < kCopyStreams; ++s)
         if (need[s] > P.waited[s]) {
             CZ_CHECK(hipStreamWaitEvent(st, P.slot_ev[at[s]], 0), -4);
             P.waited[s] = need[s];
@@ -2550,11 +2561,13 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
         memcpy(L.slot_map_stage, L.slot_map.data(), L.slot_map.size() * sizeof(int32_t));
         CZ_CHECK(hipEventRecord(P.ev_copy_hi, P.copy_hi), -4);  // behind the demand fills too
         CZ_CHECK(hipStreamWaitEvent(P.copy, P.ev_copy_hi, 0), -4);
+        CZ_CHECK(hipEventRecord(P.ev_copy2, P.copy2), -4);  // and the other prefetch stream's
+        CZ_CHECK(hipStreamWaitEvent(P.copy, P.ev_copy2, 0), -4);
         CZ_CHECK(hipMemcpyAsync(L.slot_map_dev, L.slot_map_stage, L.slot_map.size() * sizeof(int32_t),
                                 hipMemcpyHostToDevice, P.copy), -3);
         CZ_CHECK(hipEventRecord(P.ev_copy, P.copy), -4);
         CZ_CHECK(hipStreamWaitEvent(st, P.ev_copy, 0), -4);
-        P.waited[0] = P.waited[1] = P.fill_counter;
+        P.all_waited();
     }
     return 0;
 }
@@ -3094,9 +3107,11 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
     if (!P.copy) {
         CZ_CHECK(hipStreamCreateWithFlags(&P.copy, hipStreamNonBlocking), -4);
         CZ_CHECK(hipStreamCreateWithFlags(&P.copy_hi, hipStreamNonBlocking), -4);
+        CZ_CHECK(hipStreamCreateWithFlags(&P.copy2, hipStreamNonBlocking), -4);
         CZ_CHECK(hipEventCreateWithFlags(&P.ev_idx, hipEventDisableTiming), -4);
         CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy, hipEventDisableTiming), -4);
         CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy_hi, hipEventDisableTiming), -4);
+        CZ_CHECK(hipEventCreateWithFlags(&P.ev_copy2, hipEventDisableTiming), -4);
     }
     P.d = d;
     P.w_slot = w_slot;
@@ -3110,7 +3125,8 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
     }
     P.fill_seq.assign(n, 0);
     P.fill_sid.assign(n, 0);
-    P.fill_counter = P.waited[0] = P.waited[1] = 0;
+    P.fill_counter = 0;
+    P.all_waited();
     P.key.assign(n, 0);
     P.used.assign(n, 0);
     P.prefetched.assign(n, 0);
@@ -3133,6 +3149,7 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     CZ_CHECK(hipStreamSynchronize(g.stream), -5);
     CZ_CHECK(hipStreamSynchronize(P.copy), -5);
     CZ_CHECK(hipStreamSynchronize(P.copy_hi), -5);
+    CZ_CHECK(hipStreamSynchronize(P.copy2), -5);
     for (auto it = g.layers.begin(); it != g.layers.end();) {
         if (it->second.streamed()) {
             free_layer(it->second);
@@ -3156,7 +3173,8 @@ extern "C" int colizig_hip_stream_pool_free(void) {
     P.next_stats = cz::PredStats{};
     P.tok_ids.clear();
     P.tok_stats = cz::PredStats{};
-    P.fill_counter = P.waited[0] = P.waited[1] = 0;
+    P.fill_counter = 0;
+    P.all_waited();
     P.hits = P.misses = P.loads = P.evictions = P.prefetch_issued = P.prefetch_hits = P.prefetch_wasted =
         P.bytes_h2d = P.spec_layers = P.spec_stops = 0;
     P.log.clear();
@@ -3175,6 +3193,7 @@ int stream_layer_setup(LayerHost *L, uint32_t layer) {
     (void)hipStreamSynchronize(g.stream);
     (void)hipStreamSynchronize(P.copy);
     (void)hipStreamSynchronize(P.copy_hi);
+    (void)hipStreamSynchronize(P.copy2);
     if (!L->streamed()) {
         if (L->ew) (void)hipFree(L->ew);
         if (L->es) (void)hipFree(L->es);
@@ -3362,7 +3381,8 @@ extern "C" int colizig_hip_stream_warm(uint32_t layer0, uint32_t nlayers, uint32
     }
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
     CZ_CHECK(hipStreamSynchronize(P.copy_hi), -3);
-    P.waited[0] = P.waited[1] = P.fill_counter;  // every fill is complete
+    CZ_CHECK(hipStreamSynchronize(P.copy2), -3);
+    P.all_waited();  // every fill is complete
     return (int)warmed;
 }
 
@@ -3375,13 +3395,14 @@ extern "C" int colizig_hip_stream_evict_all(void) {
     if (!g.inited || !P.on) return -1;
     CZ_CHECK(hipStreamSynchronize(P.copy), -3);
     CZ_CHECK(hipStreamSynchronize(P.copy_hi), -3);
+    CZ_CHECK(hipStreamSynchronize(P.copy2), -3);
     CZ_CHECK(hipStreamSynchronize(g.stream), -3);
     for (uint32_t i = 0; i < P.nslots; ++i) {
         P.key[i] = 0;
         P.prefetched[i] = 0;
     }
     P.where.clear();
-    P.waited[0] = P.waited[1] = P.fill_counter;  // every fill is complete
+    P.all_waited();  // every fill is complete
     P.sched.clear();
     P.pred_ids.clear();
     P.tok_ids.clear();

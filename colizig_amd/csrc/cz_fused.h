@@ -258,6 +258,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     __shared__ uint32_t s_pe[CZ_MAX_K];                     // predicted expert of each slot
     __shared__ uint32_t s_fp[CZ_MAX_K];                     // pick position of each slot's expert
     __shared__ uint32_t s_rl;                               // slots whose rows load after the routing (bits)
+    __shared__ int32_t s_slot[STOP ? 128 : 1];              // STOP: the layer's slot map (E <= 128)
 
     uint32_t xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -295,6 +296,8 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
                 for (uint32_t x = 0; x < CZ_NXCD; ++x) pv[q][x] = p4[x * H4 + min(tid + 256 * q, H4 - 1)];
             }
         }
+        int32_t sm = 0;
+        if constexpr (STOP) sm = L.slot_map[min(tid, E - 1)];  // to LDS before B1
         cz_f4 rr[QR];
         {
             const cz_f4 *src = reinterpret_cast<const cz_f4 *>(L.router) + (uint64_t)min(e0, E - 1) * H4;
@@ -319,6 +322,8 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         }
         ss = cz_wave_sum_f64_dpp(ss);
         if (lane == 0) s_ss[wave] = ss;
+        if constexpr (STOP)
+            if (tid < E) s_slot[tid] = sm;
         // router rows to LDS, chain-major (rows past ne are never read)
 #pragma unroll
         for (uint32_t q = 0; q < QR; ++q) {
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         // the same logits, so every one of them stops; the weight waves see
         // stage 3 and end too.
         if constexpr (STOP) {
-            const bool miss = lane < K && L.slot_map[o_id] < 0;
+            const bool miss = lane < K && s_slot[o_id] < 0;
             if (__builtin_amdgcn_ballot_w64(miss) != 0) {  // wave-uniform
                 if (lane == 0) {
                     if (blockIdx.x == 0) atomicCAS(A.stop, 0u, A.stop_code);
@@ -494,6 +499,13 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     // 0..K-1 of pz until the routing is known, then the routed one
     uint32_t pz = 0;
     bool routed = !SPEC;
+    // an expert's slot: with STOP from the LDS copy of the slot map (valid
+    // after B1; a missing slot reads slot 0, in bounds, and never reaches a
+    // product: the run stops)
+    auto slot_of = [&](uint32_t e) __attribute__((always_inline)) -> uint64_t {
+        if constexpr (STOP) return (uint64_t)max(s_slot[e], 0);
+        else return cz_slot(L, e);
+    };
     auto expert_of = [&](uint32_t z) __attribute__((always_inline)) -> uint32_t {
         if (routed) return min(s_idx[s_fp[z]], E - 1);
         return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(z << 2), (int)pz);
@@ -506,7 +518,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         for (uint32_t k = 0; k < NSQ; ++k) {
             const uint32_t t = min(lane + 64 * k, NSG - 1), r = t / (2 * NBH), m = (t / NBH) & 1, b = t % NBH;
             const uint32_t g = xcd + CZ_NXCD * r, z = min(g / NBI, K - 1), jj = (g - (g / NBI) * NBI) * CZ_BLOCK + rib;
-            const uint64_t sl = cz_slot(L, expert_of(z));
+            const uint64_t sl = slot_of(expert_of(z));
             scg[k] = L.es[sl * L.es_stride + (uint64_t)m * L.nbI * L.nbH + (uint64_t)(jj / CZ_BLOCK) * L.nbH + b];
         }
     };
@@ -514,7 +526,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     auto load_down_scale = [&]() __attribute__((always_inline)) {
         const uint32_t t = min(lane, (uint32_t)RW - 1);
         const uint32_t g = xcd + CZ_NXCD * t, z = min(g / NBI, K - 1), col = (g - (g / NBI) * NBI) * CZ_BLOCK;
-        const uint64_t sl = cz_slot(L, expert_of(z));
+        const uint64_t sl = slot_of(expert_of(z));
         scv = L.es[sl * L.es_stride + 2ull * L.nbI * L.nbH + (uint64_t)(r0 / CZ_BLOCK) * L.nbI + col / CZ_BLOCK];
     };
     auto load_row = [&](int r) __attribute__((always_inline)) {
@@ -554,7 +566,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     __syncthreads();  // B2
     if constexpr (SPEC) {  // the predicted experts' rows
 #pragma unroll
-        for (int r = 0; r < RW; ++r) slr[r] = cz_slot(L, (uint32_t)__builtin_amdgcn_readlane((int)pz, (int)zr[r]));
+        for (int r = 0; r < RW; ++r) slr[r] = slot_of((uint32_t)__builtin_amdgcn_readlane((int)pz, (int)zr[r]));
         load_scales();
         load_down_scale();
 #pragma unroll
@@ -631,7 +643,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         } else {
 #pragma unroll
             for (int r = 0; r < RW; ++r)
-                if ((rl >> zr[r]) & 1u) slr[r] = cz_slot(L, min(s_idx[s_fp[zr[r]]], E - 1));
+                if ((rl >> zr[r]) & 1u) slr[r] = slot_of(min(s_idx[s_fp[zr[r]]], E - 1));
             load_scales();
             load_down_scale();
 #pragma unroll
