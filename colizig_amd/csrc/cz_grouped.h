@@ -74,7 +74,7 @@ struct GroupArgs {
     uint32_t sgate_ready;      // 1: the RMS rows kernel already wrote sgate
     unsigned long long *usage; // [E] routed-selection counters to bump, or null: k_route_tokens
                                // bumps one counter per pick (one atomic each, for S = 1),
-                               // k_dispatch adds each expert's count of the round (one atomic
+                               // k_dispatch adds each expert's count of the launch (one atomic
                                // per routed expert, for S > 1: a hot expert picked by most
                                // tokens would otherwise serialise hundreds of atomics on one
                                // address); null in a routing pass whose picks another kernel
@@ -169,57 +169,37 @@ __global__ __launch_bounds__(256) void k_route_tokens(GroupArgs G) {
 }
 
 // ---------------------------------------------------------------------------
-// dispatch: one workgroup of 1024 threads (16 waves) over the S*K slot ids
-// (S*K <= CZ_DISPATCH_MAX, E <= CZ_MAX_E).  Counts by LDS integer atomics
-// (order-independent), offsets by one prefix, then a stable placement in
-// rounds of R slots: a bitmap per expert marks the round's slots of that
-// expert (bit = slot - round start), an exclusive popcount prefix over each
-// expert's words gives every slot its rank among the round's equal ids in
-// slot order, and per-expert running bases carry the earlier rounds.  Within
-// an expert, rows keep slot order.  R is the largest power of two <= 8192
-// with E * R bits in CZ_DISPATCH_WORDS words (R >= 512 for E <= 1024).
+// dispatch (moe.zig:597-612: the routed rows grouped by expert): one
+// workgroup of 1024 threads (16 waves) over the S*K slot ids (S*K <=
+// CZ_DISPATCH_MAX, E <= CZ_MAX_E).  Each slot takes its rank among its
+// expert's rows from an LDS atomic on the expert's count, the offsets come
+// from one prefix of the counts, and the slot goes to offset + rank.  Rows of
+// one expert come in the order the atomics were served, which is not fixed;
+// no result depends on it (a row's products do not depend on the other rows
+// of its M-tile, and the combine reads each slot's row through slot_pos).
 // ---------------------------------------------------------------------------
 #define CZ_DISPATCH_MAX 8192
-#define CZ_DISPATCH_WORDS 16384
 
 __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
     const LayerDev &L = G.L;
     const uint32_t E = L.E, SK = (uint32_t)G.S * L.K;
-    __shared__ uint16_t s_slot_e[CZ_DISPATCH_MAX];
-    // [E][R/32 + 1]: the round's slots of each expert, rows padded to an odd
-    // stride so the same word of different experts falls in different banks
-    __shared__ uint32_t s_bits[CZ_DISPATCH_WORDS + CZ_MAX_E];
-    __shared__ uint16_t s_pre[CZ_DISPATCH_WORDS + CZ_MAX_E];  // set bits of the expert's earlier words
+    constexpr uint32_t NQ = CZ_DISPATCH_MAX / 1024;
     __shared__ uint32_t s_cnt[CZ_MAX_E];
     __shared__ uint32_t s_off[CZ_MAX_E + 1];
-    __shared__ uint32_t s_run[CZ_MAX_E];            // rows placed so far per expert
     const uint32_t tid = threadIdx.x, lane = cz_lane();
-    uint32_t R = CZ_DISPATCH_MAX;
-    while (E * (R / 32u) > CZ_DISPATCH_WORDS) R >>= 1;
-    const uint32_t WPE = R / 32u;    // words per expert: 16..256, a power of two
-    const uint32_t TPE = WPE / 16u;  // threads per expert (16 words each): 1..16, a power of two
-    const uint32_t RS = WPE + 1u;    // row stride of s_bits / s_pre
     // the slots' expert ids: all of a thread's loads in flight at once
-    // (SK <= CZ_DISPATCH_MAX = 8 * 1024; indices past SK re-read slot SK - 1,
-    // unconditionally, so the loads are not serialised by branches)
-    uint32_t ev[CZ_DISPATCH_MAX / 1024];
+    // (indices past SK re-read slot SK - 1, unconditionally, so the loads are
+    // not serialised by branches)
+    uint32_t ev[NQ], rk[NQ];
 #pragma unroll
-    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) ev[q] = G.idx[min(tid + 1024u * q, SK - 1)];
+    for (uint32_t q = 0; q < NQ; ++q) ev[q] = G.idx[min(tid + 1024u * q, SK - 1)];
 #pragma unroll
-    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) ev[q] = min(ev[q], E - 1);
-    for (uint32_t i = tid; i < E; i += blockDim.x) {
-        s_cnt[i] = 0;
-        s_run[i] = 0;
-    }
+    for (uint32_t q = 0; q < NQ; ++q) ev[q] = min(ev[q], E - 1);
+    for (uint32_t i = tid; i < E; i += blockDim.x) s_cnt[i] = 0;
     __syncthreads();
 #pragma unroll
-    for (uint32_t q = 0; q < CZ_DISPATCH_MAX / 1024; ++q) {
-        const uint32_t i = tid + 1024u * q;
-        if (i < SK) {
-            s_slot_e[i] = (uint16_t)ev[q];
-            atomicAdd(&s_cnt[ev[q]], 1u);
-        }
-    }
+    for (uint32_t q = 0; q < NQ; ++q)
+        if (tid + 1024u * q < SK) rk[q] = atomicAdd(&s_cnt[ev[q]], 1u);
     __syncthreads();
     if (tid < 64) {  // one wave: exclusive prefix of counts and of M-tile counts
         uint32_t acc = 0, tacc = 0;
@@ -255,46 +235,14 @@ __global__ __launch_bounds__(1024) void k_dispatch(GroupArgs G) {
             if (G.usage && s_cnt[e]) atomicAdd(G.usage + e, (unsigned long long)s_cnt[e]);
         }
     }
-    const uint32_t nw = E * RS;  // bitmap words in use (<= CZ_DISPATCH_WORDS + CZ_MAX_E)
-    for (uint32_t r0 = 0; r0 < SK; r0 += R) {
-        const uint32_t n = min(R, SK - r0);
-        for (uint32_t x = tid; x < nw; x += blockDim.x) s_bits[x] = 0;
-        __syncthreads();
-        for (uint32_t i = tid; i < n; i += blockDim.x)
-            atomicOr(&s_bits[s_slot_e[r0 + i] * RS + (i >> 5)], 1u << (i & 31u));
-        __syncthreads();
-        // thread tid < E*TPE covers words 16k .. 16k + 15 of expert tid / TPE
-        // (k = tid % TPE); the TPE threads of an expert are consecutive lanes
-        // of one 16-lane row, so their scan is a segmented DPP scan
-        {
-            const bool act = tid < E * TPE;
-            const uint32_t w0 = act ? (tid / TPE) * RS + 16u * (tid % TPE) : 0u;
-            uint32_t c[16], tot = 0;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                c[q] = tot;
-                tot += act ? (uint32_t)__builtin_popcount(s_bits[w0 + q]) : 0u;
-            }
-            const uint32_t incl = cz_group_incl_scan_u32(tot, TPE);
-            if (act) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) s_pre[w0 + q] = (uint16_t)(incl - tot + c[q]);  // < R <= 8192
-            }
+    for (uint32_t q = 0; q < NQ; ++q) {
+        const uint32_t i = tid + 1024u * q;
+        if (i < SK) {
+            const uint32_t pos = s_off[ev[q]] + rk[q];
+            G.sorted_slot[pos] = i;
+            G.slot_pos[i] = pos;
         }
-        __syncthreads();
-        for (uint32_t i = tid; i < n; i += blockDim.x) {
-            const uint32_t e = s_slot_e[r0 + i], w = e * RS + (i >> 5);
-            const uint32_t below = s_bits[w] & ((1u << (i & 31u)) - 1u);
-            const uint32_t pos = s_off[e] + s_run[e] + s_pre[w] + (uint32_t)__builtin_popcount(below);
-            G.sorted_slot[pos] = r0 + i;
-            G.slot_pos[r0 + i] = pos;
-        }
-        __syncthreads();
-        for (uint32_t e = tid; e < E; e += blockDim.x) {
-            const uint32_t w = e * RS + WPE - 1u;
-            s_run[e] += s_pre[w] + (uint32_t)__builtin_popcount(s_bits[w]);
-        }
-        __syncthreads();
     }
 }
 
