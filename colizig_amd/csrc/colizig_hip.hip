@@ -496,7 +496,7 @@ void launch_router(const StepArgs &A, hipStream_t st) {
         return;
     }
     if (A.S >= kGroupedMinTokens && L.H % 256 == 0) {  // many tokens: RMS rows, then 16 x 16 tiles
-        if (A.rms) {
+        if (A.rms && !A.rms_ready) {
             switch ((L.H / 4 + 255) / 256) {  // 128-bit words per thread
                 case 1: k_rms_rows_wg<1><<<A.S, 256, 0, st>>>(A); break;
                 case 2: k_rms_rows_wg<2><<<A.S, 256, 0, st>>>(A); break;
@@ -734,21 +734,48 @@ int launch_shared_native_add(const LayerHost &Lh, float *out, int S, hipStream_t
     return 0;
 }
 
-int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
-                   float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+// A grouped layer's step arguments: with rms, the RMS rows also write xn's
+// f16 split (f16 GEMMs) or its three E4M3 terms (FP8 GEMMs).
+StepArgs grouped_args(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                      float *xn_trace, uint32_t *idx_trace, float *gates_trace) {
     StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
-    const LayerDev &L = A.L;
     Work &w = g.work;
-    const bool f8 = g.prefill_fp8;
-    if (rms && !f8) {  // the RMS rows kernel writes the f16 split of xn for the gate/up GEMMs
+    if (rms && !g.prefill_fp8) {
         A.xh = w.xh;
         A.xl = w.xl;
     }
-    const bool xq_rms = rms && f8 && rms_rows_wg(Lh, S);
-    if (xq_rms) {  // ... or its three E4M3 terms
+    if (rms && g.prefill_fp8 && rms_rows_wg(Lh, S)) {
         A.xq = w.xq;
         A.xe = w.xe;
     }
+    return A;
+}
+
+// Whether the combine of grouped layer Lh can form the RMS rows of the chain's
+// next layer Ln (k_combine_rms): f32 routers, no NativeMatrix shared expert
+// (whose output is added after the combine), one hidden size, and enough
+// tokens to fill the GPU with one workgroup per token (at 32 tokens the
+// combine's four workgroups per token were faster: 11.93 against 12.10 ms
+// per c4 step).
+constexpr int kCombineRmsMinTokens = 256;
+bool combine_rms_ok(const LayerHost &Lh, const LayerHost &Ln, int S) {
+    const uint32_t q = (Lh.d.hidden / 4 + 255) / 256;
+    return S >= kCombineRmsMinTokens && grouped_ok(Lh.d, S) && grouped_ok(Ln.d, S) && Ln.d.hidden == Lh.d.hidden &&
+           !Ln.router_bf16 &&
+           Lh.shn_dtype < 0 && Ln.shn_dtype < 0 && rms_rows_wg(Ln, S) && q >= 1 && q <= 8;
+}
+
+// rms_ready: the previous layer's combine wrote this layer's RMS rows; next
+// (nullable, combine_rms_ok): this layer's combine writes the next layer's.
+int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
+                   float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st, bool rms_ready = false,
+                   const LayerHost *next = nullptr, float *next_xn_trace = nullptr) {
+    StepArgs A = grouped_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
+    A.rms_ready = rms_ready ? 1u : 0u;
+    const LayerDev &L = A.L;
+    Work &w = g.work;
+    const bool f8 = g.prefill_fp8;
+    const bool xq_rms = A.xq != nullptr;
     launch_router(A, st);
     if (Lh.shn_dtype >= 0) {
         if (int rc = launch_shared_native_pre(Lh, rms ? w.xn : x, S, st)) return rc;
@@ -894,7 +921,21 @@ int launch_grouped(const LayerHost &Lh, const float *x, int S, float *out, int r
         k_gg8<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
     else
         k_gg<GG_DOWN><<<qd + gg_blocks(G.max_tiles, L.H, cd), 256, 0, st>>>(G, D, QD);
-    k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
+    if (next) {
+        const StepArgs An = grouped_args(*next, out, S, out, 1, eps, out, next_xn_trace, nullptr, nullptr);
+        switch ((L.H / 4 + 255) / 256) {
+            case 1: k_combine_rms<1><<<S, 256, 0, st>>>(G, An); break;
+            case 2: k_combine_rms<2><<<S, 256, 0, st>>>(G, An); break;
+            case 3: k_combine_rms<3><<<S, 256, 0, st>>>(G, An); break;
+            case 4: k_combine_rms<4><<<S, 256, 0, st>>>(G, An); break;
+            case 5: k_combine_rms<5><<<S, 256, 0, st>>>(G, An); break;
+            case 6: k_combine_rms<6><<<S, 256, 0, st>>>(G, An); break;
+            case 7: k_combine_rms<7><<<S, 256, 0, st>>>(G, An); break;
+            default: k_combine_rms<8><<<S, 256, 0, st>>>(G, An); break;
+        }
+    } else {
+        k_combine<<<dim3((L.H + CZ_COMBINE_COLS - 1) / CZ_COMBINE_COLS, S), 256, 0, st>>>(G);
+    }
     if (Lh.shn_dtype >= 0) {
         if (int rc = launch_shared_native_add(Lh, out, S, st)) return rc;
     }
@@ -1076,9 +1117,11 @@ int chain_fused_prepare(uint32_t layer0, uint32_t n, int S) {
 }
 
 int launch_layer(const LayerHost &Lh, const float *x, int S, float *out, int rms, float eps, const float *xres,
-                 float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st) {
+                 float *xn_trace, uint32_t *idx_trace, float *gates_trace, hipStream_t st, bool rms_ready = false,
+                 const LayerHost *next = nullptr, float *next_xn_trace = nullptr) {
     if (grouped_ok(Lh.d, S))
-        return launch_grouped(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace, st);
+        return launch_grouped(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace, st, rms_ready, next,
+                              next_xn_trace);
     const StepArgs A = step_args(Lh, x, S, out, rms, eps, xres, xn_trace, idx_trace, gates_trace);
     if (Lh.shn_dtype < 0) return launch_step(A, st);
     int rc = launch_step(A, st, kRouter);
@@ -2004,13 +2047,19 @@ static int chain_enqueue(uint32_t layer0, uint32_t nlayers, float *x_dev, int S,
     const int fz = chain_fused_prepare(layer0, nlayers, S);
     if (fz < 0) return fz;
     if (fz) return chain_enqueue_fused(layer0, nlayers, x_dev, eps, xn_trace, idx_trace, gates_trace, st);
+    // grouped layers: each layer's combine forms the next layer's RMS rows
+    bool ready = false;
     for (uint32_t l = 0; l < nlayers; ++l) {
         LayerHost *L = find_layer(layer0 + l);
+        const LayerHost *N = l + 1 < nlayers ? find_layer(layer0 + l + 1) : nullptr;
+        if (N && !combine_rms_ok(*L, *N, S)) N = nullptr;
         const size_t sh = (size_t)S * L->d.hidden, sk = (size_t)S * L->d.topk;
         const int rc = launch_layer(*L, x_dev, S, x_dev, 1, eps, x_dev, xn_trace ? xn_trace + l * sh : nullptr,
                                     idx_trace ? idx_trace + l * sk : nullptr,
-                                    gates_trace ? gates_trace + l * sk : nullptr, st);
+                                    gates_trace ? gates_trace + l * sk : nullptr, st, ready, N,
+                                    N && xn_trace ? xn_trace + (l + 1) * sh : nullptr);
         if (rc) return rc;
+        ready = N != nullptr;
     }
     return 0;
 }

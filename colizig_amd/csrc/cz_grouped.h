@@ -968,3 +968,66 @@ __global__ __launch_bounds__(256) void k_combine(GroupArgs G) {
     r.w = r.w + ys.w;
     *(float4 *)(G.out + o) = r;
 }
+
+// The combine of one token's whole row (thread tid: float4 columns tid +
+// 256 k, each formed as k_combine forms it), then the next layer's RMS rows
+// of that row (cz_rms_row_tail with the next layer's arguments An): one
+// launch fewer per layer of a chain, and the row is not read back.
+template <int Q>
+__global__ __launch_bounds__(256) void k_combine_rms(GroupArgs G, StepArgs An) {
+    __shared__ __align__(16) float s_row[Q * 1024];
+    __shared__ float s_inv;
+    const LayerDev &L = G.L;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, n4 = L.H / 4;
+    const uint64_t H = L.H;
+    const uint32_t *order = G.tok_order + (uint64_t)t * L.K;
+    const float sg = L.SI != 0 ? G.sgate[t] : 0.0f;  // read before the tail writes the next layer's
+    float4 r[Q];
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k) {
+        const uint32_t q = min(tid + 256 * k, n4 - 1);  // clamped: in bounds, not stored
+        const uint32_t d = 4u * q;
+        float4 ys = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (L.SI != 0) {
+            const float4 v = *(const float4 *)(G.os + t * H + d);
+            ys.x = ys.x + sg * v.x;
+            ys.y = ys.y + sg * v.y;
+            ys.z = ys.z + sg * v.z;
+            ys.w = ys.w + sg * v.w;
+        }
+        for (uint32_t z0 = 0; z0 < L.K; z0 += 8) {
+            uint32_t sl[8], pos[8];
+            float g[8];
+            float4 v[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) sl[i] = cz_const_u32(order + min(z0 + i, L.K - 1));
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                g[i] = cz_const_f32(G.gates + sl[i]);
+                pos[i] = cz_const_u32(G.slot_pos + sl[i]);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) v[i] = *(const float4 *)(G.o + (uint64_t)pos[i] * H + d);
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                if (z0 + i < L.K) {
+                    ys.x = ys.x + g[i] * v[i].x;
+                    ys.y = ys.y + g[i] * v[i].y;
+                    ys.z = ys.z + g[i] * v[i].z;
+                    ys.w = ys.w + g[i] * v[i].w;
+                }
+            }
+        }
+        const uint64_t o = t * H + d;
+        float4 x = G.xres ? *(const float4 *)(G.xres + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        x.x = x.x + ys.x;
+        x.y = x.y + ys.y;
+        x.z = x.z + ys.z;
+        x.w = x.w + ys.w;
+        r[k] = x;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k)
+        if (tid + 256 * k < n4) *(float4 *)(G.out + t * H + 4u * (tid + 256 * k)) = r[k];
+    cz_rms_row_tail<Q>(An, t, r, s_row, &s_inv);
+}

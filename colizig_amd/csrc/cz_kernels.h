@@ -130,6 +130,7 @@ struct StepArgs {
     // the routing, so the layer and every later one leave x as it was.
     uint32_t *stop;
     uint32_t stop_code;
+    uint32_t rms_ready;    // 1: the previous layer's combine already wrote xn (and its GEMM terms)
     int S;
     int tt;                // router tokens per tile (1..CZ_ROUTER_TT)
     int rms;
@@ -508,22 +509,23 @@ __device__ __forceinline__ void cz_q3_group4(float (&r)[4], uint8_t *q, uint64_t
 // a shared expert, wave 1 also forms its gate sigmoid(xn . sh_gate) in
 // cz_sgate_dot's order (lane l: columns l, l + 64, ... increasing, then the
 // DPP wave sum), its sh_gate elements requested with the row.
+// The RMS rows of token `t` from its row v (thread tid holds float4 tid +
+// 256 k): the row staged in LDS, the sum of squares by one wave in the decode
+// order, then xn (and its f16 split or E4M3 terms, the shared-expert gate)
+// written for A's layer.  Shared by k_rms_rows_wg and the combine that forms
+// the next layer's rows (k_combine_rms).
 template <int Q>
-__global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
-    __shared__ __align__(16) float s_row[Q * 1024];
-    __shared__ float s_inv;
+__device__ __forceinline__ void cz_rms_row_tail(const StepArgs &A, uint32_t t, float4 (&v)[Q], float *s_row,
+                                                float *s_inv_p) {
     const uint32_t H = A.L.H, n4 = H / 4, tid = threadIdx.x, nq = H / 64;
-    const uint64_t row = (uint64_t)blockIdx.x * H;
-    const float4 *x4 = reinterpret_cast<const float4 *>(A.x + row);
+    const uint64_t row = (uint64_t)t * H;
     const bool gate = A.L.SI != 0 && (tid >> 6) == 1;  // wave-uniform
     float g[16 * Q];
     if (gate) {
 #pragma unroll
         for (uint32_t i = 0; i < 16 * Q; ++i) g[i] = A.L.sh_gate[(tid & 63) + 64 * min(i, nq - 1)];  // clamped
     }
-    float4 v[Q];
-#pragma unroll
-    for (uint32_t k = 0; k < Q; ++k) v[k] = x4[min(tid + 256 * k, n4 - 1)];  // clamped: in bounds
+    float &s_inv = *s_inv_p;
 #pragma unroll
     for (uint32_t k = 0; k < Q; ++k)
         if (tid + 256 * k < n4) reinterpret_cast<float4 *>(s_row)[tid + 256 * k] = v[k];
@@ -551,7 +553,7 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
             d = i < nq ? dn : d;
         }
         d = cz_wave_sum_dpp(d);
-        if (l == 0) A.sgate[blockIdx.x] = cz_sigmoid(d);
+        if (l == 0) A.sgate[t] = cz_sigmoid(d);
     }
     typedef _Float16 cz_half4 __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -570,10 +572,22 @@ __global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
         }
         if (A.xq) {  // the group of 32 columns is 8 consecutive lanes (H % 32 == 0: whole groups active)
             float r[4] = {y.x, y.y, y.z, y.w};
-            cz_q3_group4(r, A.xq + row + 4 * q, (uint64_t)A.S * H, A.xe + (uint64_t)blockIdx.x * (H / 32) + q / 8,
+            cz_q3_group4(r, A.xq + row + 4 * q, (uint64_t)A.S * H, A.xe + (uint64_t)t * (H / 32) + q / 8,
                          (uint64_t)A.S * (H / 32), (q & 7u) == 0, true);
         }
     }
+}
+
+template <int Q>
+__global__ __launch_bounds__(256) void k_rms_rows_wg(StepArgs A) {
+    __shared__ __align__(16) float s_row[Q * 1024];
+    __shared__ float s_inv;
+    const uint32_t n4 = A.L.H / 4, tid = threadIdx.x;
+    const float4 *x4 = reinterpret_cast<const float4 *>(A.x + (uint64_t)blockIdx.x * A.L.H);
+    float4 v[Q];
+#pragma unroll
+    for (uint32_t k = 0; k < Q; ++k) v[k] = x4[min(tid + 256 * k, n4 - 1)];  // clamped: in bounds
+    cz_rms_row_tail<Q>(A, blockIdx.x, v, s_row, &s_inv);
 }
 
 // Rows longer than the workgroup form holds: one wave per token.
