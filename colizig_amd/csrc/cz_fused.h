@@ -49,6 +49,9 @@
 #define CZ_FWG (CZ_NXCD * CZ_WPX)       // workgroups per layer launch
 #define CZ_FEPW 4                       // router rows per workgroup (E <= 128)
 #define CZ_FPOLL_TICKS 2000000ll        // poll limit: 20 ms of the 100 MHz wall clock
+#ifndef CZ_PRED_EARLY
+#define CZ_PRED_EARLY 1                 // predicted gate/up rows a weight wave requests before the logit poll
+#endif
 
 // error bits (host word)
 #define CZ_FERR_TIMEOUT 1u
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     __shared__ uint32_t s_pe[CZ_MAX_K];                     // predicted expert of each slot
     __shared__ uint32_t s_fp[CZ_MAX_K];                     // pick position of each slot's expert
     __shared__ uint32_t s_rl;                               // slots whose rows load after the routing (bits)
+    __shared__ uint32_t s_lgp;                              // 1: wave 0 has polled the XCD's logits
     __shared__ int32_t s_slot[STOP ? 128 : 1];              // STOP: the layer's slot map (E <= 128)
 
     uint32_t xcc;
@@ -268,7 +272,10 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
     const uint32_t ptag = tag & A.poll_mask;  // the tag this layer's polls wait for
     const uint32_t e0 = w * CZ_FEPW;
     const uint32_t ne = E > e0 ? min((uint32_t)CZ_FEPW, E - e0) : 0u;
-    if (tid == 0) s_stage = 0;
+    if (tid == 0) {
+        s_stage = 0;
+        s_lgp = 0;
+    }
 
     if (wave < 4) {
         // ================= control waves (threads 0..255) =================
@@ -395,6 +402,7 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         // single-wave routing of the decode kernels: no workgroup barrier)
         float lg[2] = {0.0f, 0.0f};
         cz_poll_tagged<2>(A.lgx + (uint64_t)xcd * E, E, ptag, lg, A.err);
+        if (lane == 0) __hip_atomic_store(&s_lgp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         uint32_t o_pos = 0, o_id = 0;
         float o_gate = 0.0f;
         cz_route_wave_regs<2>(lg, E, K, L.norm_topk, s_idx, s_gate, o_pos, o_id, o_gate);
@@ -569,8 +577,15 @@ __global__ __launch_bounds__(512) void k_layer_fused(FusedArgs A) {
         for (int r = 0; r < RW; ++r) slr[r] = slot_of((uint32_t)__builtin_amdgcn_readlane((int)pz, (int)zr[r]));
         load_scales();
         load_down_scale();
+        // the first rows now, the rest once the logits are polled: a poll's
+        // round trip waits behind every request already in the CU's memory
+        // pipeline
+        constexpr int RE = CZ_PRED_EARLY < RW ? CZ_PRED_EARLY : RW;
 #pragma unroll
-        for (int r = 0; r < RW; ++r) load_row(r);
+        for (int r = 0; r < RE; ++r) load_row(r);
+        if constexpr (RE < RW) cz_lds_wait(&s_lgp, 1u, A.err);
+#pragma unroll
+        for (int r = RE; r < RW; ++r) load_row(r);
 #pragma unroll
         for (int i = 0; i < RW; ++i) load_down(i);
     }
