@@ -38,9 +38,9 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # HBM bytes per launch of the one-launch layer kernel on this workload,
 # measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE and scaled by
 # what the same counters read for a plain 256 MiB copy (FETCH_SIZE x 2.0,
-# WRITE_SIZE x 1.0): 24431.5 KiB fetched, 134.5 KiB written per dispatch
+# WRITE_SIZE x 1.0): 24430.4 KiB fetched, 134.5 KiB written per dispatch
 # (the mean over a step's 47 launches with predicted experts and its first).
-LAYER_TRAFFIC_BYTES = int(round((24431.5 * 2.0 + 134.5) * 1024))
+LAYER_TRAFFIC_BYTES = int(round((24430.4 * 2.0 + 134.5) * 1024))
 
 # HBM bytes per 512-token prefill step (48 layers x the seven kernels of a
 # layer), measured the same way: 264082.5 KiB fetched and 54035.2 KiB
