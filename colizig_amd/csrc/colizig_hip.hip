@@ -7,6 +7,7 @@
 // the engine's CPU float math.
 #include "cz_grouped.h"
 #include "cz_fused.h"
+#include "cz_lru.h"
 #include "cz_sched.h"
 #include "cz_plan.h"
 #include "colizig_hip.h"
@@ -211,6 +212,7 @@ struct StreamPool {
     }
     cz::LastTokenPredictor last_pred{8};
     cz::Scheduler sched{kSchedCapacity};
+    cz::SlotLru lru;                   // held slots in order of last use, and the free ones
     bool log_on = false;
     std::vector<uint32_t> log;         // policy ops, 4 words each (op, layer, expert, result)
     // counters (CacheStats, moe.zig:121-139)
@@ -2462,21 +2464,12 @@ uint8_t *slot_w(uint32_t i) { return g.pool.base + (uint64_t)i * g.pool.slot_byt
 
 // A slot for a new entry: the first free one, else the least recently used
 // slot not pinned by the layer in flight (victimSlot, moe.zig:183-197, over
-// one pool for every streamed layer).  Returns nslots when every slot is
-// pinned.
+// one pool for every streamed layer), from the pool's use-ordered list
+// (cz_lru.h) instead of a scan of every slot's clock (5.8 us per fill at
+// 3,390 slots).  Returns nslots when every slot is pinned.
 uint32_t pool_victim() {
     StreamPool &P = g.pool;
-    uint32_t best = P.nslots;
-    uint64_t bu = ~0ull;
-    for (uint32_t i = 0; i < P.nslots; ++i) {
-        if (P.key[i] == 0) return i;
-        if (P.epoch != 0 && P.pin_epoch[i] == P.epoch) continue;
-        if (P.used[i] < bu) {
-            bu = P.used[i];
-            best = i;
-        }
-    }
-    return best;
+    return P.lru.victim([&](uint32_t i) { return P.epoch != 0 && P.pin_epoch[i] == P.epoch; });
 }
 
 // Forgets every pool entry of `layer` (re-registration).
@@ -2486,6 +2479,7 @@ void pool_drop_layer(uint32_t layer) {
         if (P.key[i] && ((P.key[i] - 1) >> 32) == layer) {
             P.where.erase(P.key[i]);
             P.key[i] = 0;
+            P.lru.release(i);
             P.prefetched[i] = 0;
         }
 }
@@ -2528,6 +2522,7 @@ int pool_fill(LayerHost &L, uint32_t layer, uint32_t e, uint32_t i, bool prefetc
     P.where[P.key[i]] = i;
     L.slot_map[e] = (int32_t)i;  // a layer's slot map holds every resident expert of it
     P.used[i] = ++P.clock;
+    P.lru.touch(i);
     P.prefetched[i] = prefetch ? P.stats_epoch + 1 : 0;
     if (prefetch) P.prefetch_issued++;
     return 0;
@@ -2577,6 +2572,7 @@ int stream_resident(LayerHost &L, uint32_t layer, const std::vector<uint32_t> &s
                 P.prefetched[i] = 0;
             }
             P.used[i] = ++P.clock;
+            P.lru.touch(i);
             P.pin_epoch[i] = P.epoch;
             L.slot_map[e] = (int32_t)i;
             pool_log(kOpGet, layer, e, i | kLogHit);
@@ -3003,6 +2999,7 @@ int spec_account(uint32_t layer, const uint32_t *picks, uint32_t K) {
             P.prefetched[i] = 0;
         }
         P.used[i] = ++P.clock;
+        P.lru.touch(i);
         P.pin_epoch[i] = P.epoch;
         pool_log(kOpGet, layer, e, i | kLogHit);
     }
@@ -3178,6 +3175,7 @@ extern "C" int colizig_hip_stream_pool_init(const colizig_dims *dims, uint64_t c
     P.all_waited();
     P.key.assign(n, 0);
     P.used.assign(n, 0);
+    P.lru.reset(n);
     P.prefetched.assign(n, 0);
     P.pin_epoch.assign(n, 0);
     P.where.clear();
@@ -3450,6 +3448,7 @@ extern "C" int colizig_hip_stream_evict_all(void) {
         P.key[i] = 0;
         P.prefetched[i] = 0;
     }
+    P.lru.reset(P.nslots);
     P.where.clear();
     P.all_waited();  // every fill is complete
     P.sched.clear();

@@ -15,6 +15,7 @@
 #include <random>
 #include <vector>
 
+#include "cz_lru.h"
 #include "cz_plan.h"
 #include "cz_sched.h"
 
@@ -129,6 +130,74 @@ static void predictor_cases() {
     CHECK(q.predict_scored(0, rows, 4) == 0 && q.predict_scored(1, rows, 1) == 1);
 }
 
+// The pool's victim choice (cz_lru.h) against a scan of every slot, as the
+// pool chose before: the first free slot, else the held slot with the lowest
+// last-use clock among those the layer in flight does not pin; nslots when
+// all are pinned.  Random fills, hits, drops and pins over small pools.
+static void lru_cases() {
+    std::mt19937_64 rng(7);
+    for (uint32_t n : {1u, 2u, 5u, 63u, 64u, 65u, 130u}) {
+        cz::SlotLru lru;
+        lru.reset(n);
+        std::vector<uint64_t> used(n, 0), pin(n, 0);
+        std::vector<uint8_t> held(n, 0);
+        uint64_t clock = 0, epoch = 0;
+        auto scan = [&]() {
+            uint32_t best = n;
+            uint64_t bu = ~0ull;
+            for (uint32_t i = 0; i < n; ++i) {
+                if (!held[i]) return i;
+                if (epoch != 0 && pin[i] == epoch) continue;
+                if (used[i] < bu) {
+                    bu = used[i];
+                    best = i;
+                }
+            }
+            return best;
+        };
+        auto pinned = [&](uint32_t i) { return epoch != 0 && pin[i] == epoch; };
+        for (int step = 0; step < 20000; ++step) {
+            const uint32_t op = (uint32_t)(rng() % 10);
+            const uint32_t i = (uint32_t)(rng() % n);
+            if (op < 4) {  // a fill into the victim, which the layer in flight then pins
+                const uint32_t v = lru.victim(pinned);
+                CHECK(v == scan());
+                if (v < n) {
+                    held[v] = 1;
+                    used[v] = ++clock;
+                    lru.touch(v);
+                    pin[v] = epoch;
+                }
+            } else if (op < 7) {  // a hit
+                if (held[i]) {
+                    used[i] = ++clock;
+                    lru.touch(i);
+                    pin[i] = epoch;
+                }
+            } else if (op < 8) {  // the entry is dropped
+                held[i] = 0;
+                lru.release(i);
+            } else {  // the next layer: a new pin epoch
+                ++epoch;
+            }
+            CHECK(lru.held(i) == (held[i] != 0));
+        }
+        // every slot held and pinned: no victim
+        ++epoch;
+        for (uint32_t i = 0; i < n; ++i) {
+            if (!held[i]) {
+                held[i] = 1;
+                used[i] = ++clock;
+                lru.touch(i);
+            }
+            pin[i] = epoch;
+        }
+        CHECK(lru.victim(pinned) == n && scan() == n);
+        lru.reset(n);
+        CHECK(lru.victim(pinned) == 0);
+    }
+}
+
 static void plan_cases() {
     const uint64_t GB = 1ull << 30;
     const colizig_dims small{512, 16, 4, 256, 0, 1}, q3{2048, 128, 8, 768, 0, 1}, q4{4096, 512, 10, 512, 4096, 1};
@@ -205,6 +274,7 @@ int main(int argc, char **argv) {
     sched_cases();
     predictor_cases();
     plan_cases();
+    lru_cases();
     loader_cases(argv[1], argv[2], argv[3]);
     std::printf("host_check: %s (%d failed checks)\n", failures ? "FAILED" : "ok", failures);
     return failures ? 1 : 0;
