@@ -32,7 +32,8 @@
 // and the workgroup's E/32 router rows' logits in dotF32 order
 // (bit-identical to the reference); the weight waves then request the
 // predicted experts' gate/up and down rows (96 KB + 48 KB at the
-// Qwen3-30B-A3B shape); control wave 0 takes the XCD's logits and routes
+// Qwen3-30B-A3B shape: the first gate/up row at once, the rest once wave 0
+// has polled the logits); control wave 0 takes the XCD's logits and routes
 // (moe.zig:435-463's strict '>' scan restated), matches the slots to the
 // picks and hands them over; the weight waves load what the prediction
 // missed, form the gated products of the XCD, and its down partial of 64
@@ -201,10 +202,13 @@ __device__ inline uint32_t cz_topk_wave(const float (&lg)[2], uint32_t E, uint32
 // one line of the row); the row's sum is taken over its 8 lanes.
 //
 // Predicted experts (SPEC): the previous layer's kernel left this layer's
-// top-k on its own router input in pred_in; the weight waves request every
-// gate/up and down row of those experts at once as soon as the router input
-// is ready, so the weights stream while the control waves compute the router
-// and the routing.  Each slot then keeps its predicted expert if the routing picked
+// top-k on its own router input in pred_in; the weight waves request the
+// gate/up and down rows of those experts as soon as the router input is
+// ready, so the weights stream while the control waves compute the router
+// and the routing: CZ_PRED_EARLY gate/up rows at once, the others (and the
+// down rows) once wave 0 has polled the XCD's logits (an LDS word), so that
+// the poll's round trip does not wait behind the whole request in the CU's
+// memory pipeline.  Each slot then keeps its predicted expert if the routing picked
 // it (matched once per pick), and a slot whose prediction missed gets a
 // picked expert that no slot predicted and loads its rows again.  The
 // routing itself, the gates and the usage counters are the layer's own; the
