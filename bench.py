@@ -42,10 +42,12 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # (the mean over a step's 47 launches with predicted experts and its first).
 LAYER_TRAFFIC_BYTES = int(round((24430.4 * 2.0 + 134.5) * 1024))
 
-# HBM bytes per 512-token prefill step (48 layers x the seven kernels of a
-# layer), measured the same way: 264082.5 KiB fetched and 54035.2 KiB
-# written per layer, the sums of the kernels' per-dispatch means.
-PREFILL_STEP_TRAFFIC_BYTES = int(round(48 * (264082.5 * 2.0 + 54035.2) * 1024))
+# HBM bytes per 512-token prefill step (48 layers: router, routing, dispatch,
+# the two grouped GEMMs and the combine, which forms the next layer's RMS
+# rows in 47 of them; the first layer's RMS rows), measured the same way:
+# 12057994.9 KiB fetched and 2593636.8 KiB written per step, the sums of the
+# kernels' per-dispatch means.
+PREFILL_STEP_TRAFFIC_BYTES = int(round((12057994.9 * 2.0 + 2593636.8) * 1024))
 
 CONFIG = dict(workload="qwen3-30b-a3b-moe-decode", layers=48, hidden=2048, experts=128, topk=8, inter=768,
               shared_inter=0, norm_topk=1, batch=1, weights="block-fp8-e4m3-128x128", seed=0)
